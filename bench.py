@@ -1,0 +1,368 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1]
+                    [--no-cpu-baseline]
+
+Prints ONE JSON line on stdout (diagnostics go to stderr). The headline
+`value` is causal GQA prefill TFLOP/s at configuration 2 (Qwen-32B shape,
+B=4, S=2048, 40/8 heads, D=128, 16-token pages over a permuted pool): a step
+is one flash_attn_paged call over the whole batch with K/V already paged in
+HBM. The same line carries the decode half of the metric under "decode":
+configuration 4 (Llama-70B shape, B=64, context U[1024,16384], 64/8 heads):
+a step appends one token per sequence and then runs decode attention over the
+full context; decode GB/s counts live K/V + q/o + block-table bytes.
+Configurations 3, 5 and 1 are reported under "extra".
+
+Per-kernel durations come from HIP events recorded on the stream the kernels
+run on (torch's current stream) around every timed launch; `roofline.achieved`
+is algorithmic work per launch / mean launch duration. The CPU baseline is the
+oracle's restatement of the reference's CPU math path
+(flashattention_custom/ops.py:37-75), timed on the host (kind "port").
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+from hrm_flashrenderer_amd import flash_attn, flash_attn_paged, paged_kv_append, workloads  # noqa: E402
+
+METRIC = "decode attn HBM GB/s + prefill TFLOP/s (fp16) on 1 MI355X; % of roofline"
+PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_info():
+    model = platform.processor()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
+def timed(step, steps, warmup, marks=1):
+    """Run `step(events)` warmup+steps times; `events` is a list of marks+1 events
+    the step records between its launches. Returns (wall_s, [[ms per segment]...])."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(marks + 1)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    segs = [[e[i].elapsed_time(e[i + 1]) for i in range(marks)] for e in evs]
+    del stream
+    return wall, segs
+
+
+def roofline(bound, work, mean_ms, traffic=None):
+    if bound == "hbm":
+        achieved = work / (mean_ms * 1e-3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    else:
+        achieved = work / (mean_ms * 1e-3) / 1e12
+        peak, unit = PEAK_MFMA_F16_TFLOPS, "TFLOP/s"
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------- configs ---
+
+def bench_prefill(w, steps, warmup, traffic_key, traffic):
+    flops = workloads.attention_flops(w)
+    qo = w.q_offsets if w.q_offsets is not None else 0
+    stream = torch.cuda.current_stream()
+
+    def step(ev):
+        if ev:
+            ev[0].record(stream)
+        flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, w.causal, qo,
+                         block_table=w.block_table)
+        if ev:
+            ev[1].record(stream)
+
+    wall, segs = timed(step, steps, warmup)
+    durs = [s[0] for s in segs]
+    mean_ms = statistics.fmean(durs)
+    return {
+        "value": round(flops * steps / wall / 1e12, 2), "unit": "TFLOP/s",
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "kernel_ms": {"mean": round(mean_ms, 4), "median": round(statistics.median(durs), 4),
+                      "min": round(min(durs), 4), "max": round(max(durs), 4)},
+        "flops_per_step": flops,
+        "roofline": roofline("mfma", flops, mean_ms, traffic.get(traffic_key)),
+        "workload": workloads.sample_meta(w),
+    }
+
+
+def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None):
+    """Decode (+ append when the workload has new tokens). `rotate` is a second
+    workload with its own pool, alternated per step to defeat the 256 MB MALL."""
+    nbytes = workloads.decode_bytes(w)
+    abytes = workloads.append_bytes(w) if w.k_new is not None else 0.0
+    pools = [w] + ([rotate] if rotate is not None else [])
+    stream = torch.cuda.current_stream()
+    it = [0]
+
+    def step(ev):
+        x = pools[it[0] % len(pools)]
+        it[0] += 1
+        if ev:
+            ev[0].record(stream)
+        if x.k_new is not None:
+            paged_kv_append(x.k_pool, x.v_pool, x.k_new, x.v_new, x.append_pos, 16,
+                            block_table=x.block_table)
+        if ev:
+            ev[1].record(stream)
+        flash_attn_paged(x.q, x.k_pool, x.v_pool, x.seqlen, 16, x.head_map, False,
+                         block_table=x.block_table)
+        if ev:
+            ev[2].record(stream)
+
+    wall, segs = timed(step, steps, warmup, marks=2)
+    dec = [s[1] for s in segs]
+    app = [s[0] for s in segs]
+    mean_dec = statistics.fmean(dec)
+    out = {
+        "value": round(nbytes * steps / wall / 1e9, 2) if abytes == 0 else
+        round((nbytes + abytes) * steps / wall / 1e9, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "decode_kernel_ms": {"mean": round(mean_dec, 4), "median": round(statistics.median(dec), 4),
+                             "min": round(min(dec), 4), "max": round(max(dec), 4)},
+        "decode_bytes_per_step": nbytes,
+        "roofline": roofline("hbm", nbytes, mean_dec, traffic.get(traffic_key)),
+        "cache_defeat": "two pools alternated" if rotate is not None else
+                        "pool larger than the 256 MB MALL",
+        "workload": workloads.sample_meta(w),
+    }
+    if abytes:
+        mean_app = statistics.fmean(app)
+        out["append_kernel_ms"] = {"mean": round(mean_app, 4), "median": round(statistics.median(app), 4)}
+        out["append"] = roofline("hbm", abytes, mean_app, traffic.get("append"))
+        out["append_bytes_per_step"] = abytes
+        out["end_to_end_ms"] = round(statistics.fmean([a + d for a, d in zip(app, dec)]), 4)
+    return out
+
+
+def bench_cfg1(steps, warmup, dev):
+    res = {}
+    for dt in (torch.float16, torch.float32):
+        q, k, v = workloads.cfg1(dev, dt)
+        flops = workloads.causal_flops_contiguous(1, 8, 512, 512, 64)
+        stream = torch.cuda.current_stream()
+
+        def step(ev):
+            if ev:
+                ev[0].record(stream)
+            flash_attn(q, k, v)
+            if ev:
+                ev[1].record(stream)
+
+        wall, segs = timed(step, steps, warmup)
+        mean_ms = statistics.fmean(s[0] for s in segs)
+        res[str(dt).replace("torch.", "")] = {
+            "kernel_ms": round(mean_ms, 4),
+            "TFLOP/s": round(flops / (mean_ms * 1e-3) / 1e12, 3)}
+    return res
+
+
+# ------------------------------------------------------------ CPU baseline ---
+
+def cpu_baseline_paged(w, kind, budget_s=8.0):
+    """Time the oracle's restatement of the reference CPU path on this host.
+
+    The sample is a deterministic subset of sequences (and heads) chosen to fit
+    the budget, scaled to the same algorithmic unit as the GPU number."""
+    from oracle import attention as ora
+
+    threads = torch.get_num_threads()
+    q = w.q.cpu()
+    kp, vp = w.k_pool.cpu(), w.v_pool.cpu()
+    bt = w.block_table.cpu()
+    sl = w.seqlen.cpu()
+    hm = w.head_map.cpu()
+    qo = w.q_offsets.cpu() if w.q_offsets is not None else 0
+    # probe one head of the first sequence to size the sample
+    t0 = time.perf_counter()
+    ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
+                             batches=[0], heads=[0])
+    per_head0 = max(time.perf_counter() - t0, 1e-4)
+    est_total = per_head0 * w.Hq * sum(w.lengths) / max(w.lengths[0], 1)
+    if kind == "flops":
+        est_total *= max(1.0, w.M / 64)
+    frac = min(1.0, budget_s / max(est_total, 1e-6))
+    nb = max(1, min(w.B, int(round(w.B * frac))))
+    batches = list(range(nb))
+    heads = None
+    if nb == 1 and frac * w.B < 1.0:
+        nh = max(1, min(w.Hq, int(w.Hq * frac * w.B)))
+        heads = list(range(nh))
+    if w.k_new is not None:
+        kc, vc = kp.clone(), vp.clone()
+        kn, vn, ap = w.k_new.cpu(), w.v_new.cpu(), w.append_pos.cpu()
+    t0 = time.perf_counter()
+    if w.k_new is not None:
+        ora.cpu_paged_kv_append(kc, vc, kn, vn, ap, 16, block_table=bt)
+    ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
+                             batches=batches, heads=heads)
+    dt = time.perf_counter() - t0
+    nh = w.Hq if heads is None else len(heads)
+    sub_pairs = 0
+    sub_tokens = 0
+    for b in batches:
+        n = w.lengths[b]
+        sub_tokens += n
+        if w.causal:
+            off = w.q_offsets_host[b] if w.q_offsets_host else 0
+            sub_pairs += sum(max(0, min(n, off + i + 1)) for i in range(w.M))
+        else:
+            sub_pairs += w.M * n
+    if kind == "flops":
+        value = 4.0 * w.D * sub_pairs * nh / dt / 1e12
+        unit = "TFLOP/s"
+    else:
+        sub_bytes = sub_tokens * w.Hk * w.D * 2 * 2 * nh / w.Hq + 2 * len(batches) * nh * w.M * w.D * 2
+        value = sub_bytes / dt / 1e9
+        unit = "GB/s"
+    sample = f"sequences {batches[0]}..{batches[-1]} of {w.B}"
+    sample += f", heads 0..{nh - 1} of {w.Hq}" if heads is not None else f", all {w.Hq} heads"
+    sample += f"; {dt:.2f} s on the host"
+    return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port",
+            "sample": sample, "cpu": cpu_info(), "torch": torch.__version__}
+
+
+# -------------------------------------------------------------------- main ---
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="2,4,3,5,1")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "bench.py measures one GPU: this attention path runs on a "
+                                   "single MI355X (no sharding, no collectives); use --gpus 1"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
+    traffic = load_traffic()
+    K, W = args.steps, args.warmup
+    result = {}
+    extra = {}
+    cpu = {}
+
+    if "2" in cfgs:
+        log("cfg2: building workload")
+        w2 = workloads.cfg2(dev)
+        result = bench_prefill(w2, K, W, "prefill_cfg2", traffic)
+        log(f"cfg2: {result['value']} TFLOP/s, kernel {result['kernel_ms']['mean']} ms")
+        if not args.no_cpu_baseline:
+            cpu["cfg2"] = cpu_baseline_paged(w2, "flops")
+            log(f"cfg2 cpu: {cpu['cfg2']}")
+        del w2
+    if "4" in cfgs:
+        log("cfg4: building workload")
+        w4 = workloads.cfg4(dev)
+        extra["decode_cfg4"] = bench_decode(w4, K, W, "decode_cfg4", traffic)
+        log(f"cfg4: decode {extra['decode_cfg4']['roofline']['achieved']} GB/s")
+        if not args.no_cpu_baseline:
+            cpu["cfg4"] = cpu_baseline_paged(w4, "bytes")
+            log(f"cfg4 cpu: {cpu['cfg4']}")
+        del w4
+    if "3" in cfgs:
+        log("cfg3: building workload (two pools)")
+        w3 = workloads.cfg3(dev)
+        w3b = workloads.cfg3(dev)
+        extra["decode_cfg3"] = bench_decode(w3, K, W, "decode_cfg3", traffic, rotate=w3b)
+        log(f"cfg3: decode {extra['decode_cfg3']['roofline']['achieved']} GB/s")
+        if not args.no_cpu_baseline:
+            cpu["cfg3"] = cpu_baseline_paged(w3, "bytes")
+        del w3, w3b
+    if "5" in cfgs:
+        log("cfg5: building workload")
+        w5 = workloads.cfg5(dev)
+        extra["chunked_prefill_cfg5"] = bench_prefill(w5, max(3, K // 4), min(W, 2),
+                                                      "prefill_cfg5", traffic)
+        log(f"cfg5: {extra['chunked_prefill_cfg5']['value']} TFLOP/s")
+        if not args.no_cpu_baseline:
+            cpu["cfg5"] = cpu_baseline_paged(w5, "flops", budget_s=6.0)
+        del w5
+    if "1" in cfgs:
+        extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
+    torch.cuda.synchronize()
+
+    if not result:  # prefill not requested: report the first measured config as headline
+        key = next(iter(extra))
+        result = extra.pop(key)
+    decode = extra.pop("decode_cfg4", None)
+    line = {
+        "metric": METRIC,
+        "value": result["value"],
+        "unit": result["unit"],
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": result["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, random block tables)",
+        "config": {"workload": "cfg2_prefill_qwen32b" if "2" in cfgs else "custom",
+                   **result.get("workload", {})},
+        "roofline": result["roofline"],
+        "cpu_baseline": cpu.get("cfg2"),
+        "kernel_ms": result.get("kernel_ms"),
+    }
+    if decode is not None:
+        decode["cpu_baseline"] = cpu.get("cfg4")
+        line["decode"] = decode
+    for k, v in extra.items():
+        cfg_key = {"decode_cfg3": "cfg3", "chunked_prefill_cfg5": "cfg5"}.get(k)
+        if isinstance(v, dict) and cfg_key and cfg_key in cpu:
+            v["cpu_baseline"] = cpu[cfg_key]
+    line["extra"] = extra
+    line["device"] = torch.cuda.get_device_name(0)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

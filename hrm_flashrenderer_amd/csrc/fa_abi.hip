@@ -1,0 +1,221 @@
+// extern "C" entry points of libfa_mi355x.so (declared in include/fa_mi355x.h).
+//
+// This layer replaces the reference's pybind module csrc/ext.cpp:30-116: it
+// validates sizes (with the reference's messages where the same condition is
+// checked), builds the kernel arguments and launches on the caller's stream.
+// It never allocates device memory and never synchronises the host. Errors are
+// returned as status codes; the message is kept per thread (fa_last_error).
+#include "fa_mi355x.h"
+#include "fa_common.h"
+
+#include <limits.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int launch_status(hipError_t e) {
+  if (e == hipSuccess) return FA_OK;
+  return fail(FA_ERR_LAUNCH, "HIP launch failed: %s", hipGetErrorString(e));
+}
+
+int ps_shift_of(int ps) {
+  if (ps <= 0 || (ps & (ps - 1)) != 0) return -1;
+  int s = 0;
+  while ((1 << s) < ps) ++s;
+  return s;
+}
+
+bool head_dim_ok(int D) { return D == 64 || D == 128; }
+
+// Offsets are narrowed to int as the reference launcher does ((int)q_offset,
+// csrc/flash_attn_sm75.cu:461, :519).
+int narrow(int64_t v) { return (int)v; }
+
+fa::KVMap paged_map(const int32_t* block_table, int max_blocks, int NB, int Hk, int P, int PS,
+                    int D) {
+  fa::KVMap m;
+  m.block_table = block_table;
+  m.stride_page = (int64_t)PS * D;
+  m.stride_hk = (int64_t)P * m.stride_page;
+  m.stride_nb = (int64_t)Hk * m.stride_hk;
+  m.max_blocks = block_table ? max_blocks : P;
+  m.P = P;
+  const int64_t phys = (int64_t)NB * P;
+  m.num_phys = phys > INT_MAX ? INT_MAX : (int)phys;
+  m.PS = PS;
+  m.ps_shift = ps_shift_of(PS);
+  m.D = D;
+  m.paged = 1;
+  return m;
+}
+
+int capacity_tokens(int cap_pages, int PS) {
+  const int64_t t = (int64_t)cap_pages * PS;
+  return t > INT_MAX ? INT_MAX : (int)t;
+}
+
+// Shared validation of the paged pool arguments.
+int check_pool(int B, int NB, int Hk, int P, int page_size, const int32_t* block_table,
+               int max_blocks) {
+  if (NB < 0 || Hk <= 0 || P < 0) return fail(FA_ERR_INVALID, "k_pages/v_pages [B,Hk,P,PS,D]");
+  if (page_size <= 0) return fail(FA_ERR_INVALID, "page_size mismatch");
+  if (block_table == nullptr && NB != B) return fail(FA_ERR_INVALID, "B mismatch");
+  if (block_table != nullptr && max_blocks < 0)
+    return fail(FA_ERR_INVALID, "block_table [B, max_blocks] required");
+  return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_last_error(void) { return g_last_error.c_str(); }
+
+int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                      int Hq, int Hk, int M, int N, int D, int causal, int64_t q_offset,
+                      int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
+                      void* stream) {
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_F32)
+    return fail(FA_ERR_INVALID, "fp16 or fp32 required");
+  if (B < 0 || Hq < 0 || Hk < 0 || M < 0 || N < 0 || D < 0)
+    return fail(FA_ERR_INVALID, "q/k/v must be 4D");
+  if (Hk == 0 ? Hq != 0 : (Hq % Hk) != 0) return fail(FA_ERR_INVALID, "H mismatch");
+  if (!head_dim_ok(D)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
+  if ((int64_t)B * Hq * M == 0) return FA_OK;
+  if (q == nullptr || o == nullptr || (N > 0 && (k == nullptr || v == nullptr)))
+    return fail(FA_ERR_INVALID, "null tensor pointer");
+
+  fa::AttnParams p = {};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.seqlen = nullptr;
+  p.head_map = nullptr;
+  p.q_offsets = q_offsets;
+  p.k_offsets = k_offsets;
+  p.kv.block_table = nullptr;
+  p.kv.stride_hk = (int64_t)N * D;
+  p.kv.stride_nb = (int64_t)Hk * p.kv.stride_hk;
+  p.kv.stride_page = 0;
+  p.kv.max_blocks = 0;
+  p.kv.P = 0;
+  p.kv.num_phys = 0;
+  p.kv.PS = 1;
+  p.kv.ps_shift = 0;
+  p.kv.D = D;
+  p.kv.paged = 0;
+  p.B = B;
+  p.Hq = Hq;
+  p.Hk = Hk;
+  p.M = M;
+  p.N = N;
+  p.group = Hq / Hk;
+  p.causal = causal ? 1 : 0;
+  p.q_offset = narrow(q_offset);
+  p.k_offset = narrow(k_offset);
+  p.scale_log2 = fa::kLog2e / sqrtf((float)D);
+  (void)hipGetLastError();
+  return launch_status(fa::launch_prefill(p, D, dtype, (hipStream_t)stream));
+}
+
+size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacity_pages,
+                                int page_size) {
+  if (B <= 0 || Hq <= 0 || M <= 0 || Hk <= 0 || !head_dim_ok(D)) return 0;
+  if (!fa::use_decode_path(M, Hq, Hk)) return 0;
+  const int cap = capacity_tokens(capacity_pages < 0 ? 0 : capacity_pages,
+                                  page_size < 1 ? 1 : page_size);
+  return fa::plan_decode(B, Hq, M, D, Hk, cap).ws_bytes;
+}
+
+int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
+                            const int32_t* seqlen, int page_size, const int32_t* head_map, void* o,
+                            int B, int Hq, int M, int D, int NB, int Hk, int P, int causal,
+                            int64_t q_offset, int64_t k_offset, const int32_t* q_offsets,
+                            const int32_t* k_offsets, const int32_t* block_table, int max_blocks,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
+  int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
+  if (rc != FA_OK) return rc;
+  if (!head_dim_ok(D)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
+  if ((int64_t)B * Hq * M == 0) return FA_OK;
+  if (q == nullptr || o == nullptr || seqlen == nullptr || head_map == nullptr ||
+      ((int64_t)NB * P > 0 && (k_pages == nullptr || v_pages == nullptr)))
+    return fail(FA_ERR_INVALID, "null tensor pointer");
+
+  const int PS = page_size;
+  fa::AttnParams p = {};
+  p.q = q;
+  p.k = k_pages;
+  p.v = v_pages;
+  p.o = o;
+  p.seqlen = seqlen;
+  p.head_map = head_map;
+  p.q_offsets = q_offsets;
+  p.k_offsets = k_offsets;
+  p.kv = paged_map(block_table, max_blocks, NB, Hk, P, PS, D);
+  p.B = B;
+  p.Hq = Hq;
+  p.Hk = Hk;
+  p.M = M;
+  p.N = capacity_tokens(p.kv.max_blocks, PS);
+  p.group = 1;
+  p.causal = causal ? 1 : 0;
+  p.q_offset = narrow(q_offset);
+  p.k_offset = narrow(k_offset);
+  p.scale_log2 = fa::kLog2e / sqrtf((float)D);
+
+  (void)hipGetLastError();
+  if (fa::use_decode_path(M, Hq, Hk)) {
+    const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N);
+    if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
+      return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    const size_t slots = (size_t)B * Hq * M * plan.nsplit;
+    const size_t o_bytes = ((slots * D * sizeof(float)) + 255) / 256 * 256;
+    p.ws_o = reinterpret_cast<float*>(workspace);
+    p.ws_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + o_bytes);
+    p.nsplit = plan.nsplit;
+    p.split_tokens = plan.split_tokens;
+    return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
+  }
+  return launch_status(fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream));
+}
+
+int fa_paged_kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
+                       int Hk, int T, int D, int NB, int P, int page_size, int64_t start_pos,
+                       const int32_t* start_positions, const int32_t* block_table, int max_blocks,
+                       void* stream) {
+  if (B < 0 || T < 0 || D <= 0) return fail(FA_ERR_INVALID, "shape mismatch");
+  int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
+  if (rc != FA_OK) return rc;
+  if (D % 8 != 0) return fail(FA_ERR_INVALID, "head_dim must be a multiple of 8");
+  if ((int64_t)B * Hk * T == 0) return FA_OK;
+  if (k_pages == nullptr || v_pages == nullptr || k_new == nullptr || v_new == nullptr)
+    return fail(FA_ERR_INVALID, "null tensor pointer");
+  const fa::KVMap map = paged_map(block_table, max_blocks, NB, Hk, P, page_size, D);
+  (void)hipGetLastError();
+  return launch_status(fa::launch_paged_append(k_pages, v_pages, k_new, v_new, map, B, Hk, T,
+                                               narrow(start_pos), start_positions,
+                                               (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+// Paged KV append for gfx950.
+//
+// Semantics follow the reference's paged_kv_append_kernel
+// (csrc/flash_attn_sm75.cu:528-555) and its CPU twin
+// (flashattention_custom/ops.py:66-75): token t of sequence b goes to position
+// start + t, i.e. page (start+t)/PS, slot (start+t)%PS, for every KV head.
+// Positions whose page is out of range are skipped (reference :548).
+//
+// Layout of the work: one lane moves one 16-byte chunk (8 fp16) of K and the
+// same chunk of V. Consecutive lanes take consecutive chunks of a token row,
+// then consecutive tokens, so both the source rows [B,Hk,T,D] and the
+// destination slots (consecutive within a page) are written as whole 64-byte
+// segments per quarter-wave. Work is split as (b, hk, t, chunk); when the chunk
+// count D/8 is a power of two (D = 64, 128) the chunk index is a mask and a
+// shift, otherwise a division.
+#include "fa_common.h"
+
+namespace fa {
+
+__global__ __launch_bounds__(256) void paged_append_kernel(
+    f16* __restrict__ k_pages, f16* __restrict__ v_pages,
+    const f16* __restrict__ k_new, const f16* __restrict__ v_new,
+    KVMap map, int B, int Hk, int T, int chunks_per_row, int chunk_shift, int start_pos,
+    const int32_t* __restrict__ start_positions, int64_t total_chunks) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total_chunks) return;
+  int chunk;
+  int64_t row;  // (b*Hk + hk)*T + t
+  if (chunk_shift >= 0) {
+    chunk = (int)(idx & ((1 << chunk_shift) - 1));
+    row = idx >> chunk_shift;
+  } else {
+    row = idx / chunks_per_row;
+    chunk = (int)(idx - row * chunks_per_row);
+  }
+  const int t = (int)(row % T);
+  const int64_t bh = row / T;
+  const int hk = (int)(bh % Hk);
+  const int b = (int)(bh / Hk);
+
+  const int start = start_positions ? start_positions[b] : start_pos;
+  const int pos = start + t;
+  if (pos < 0) return;
+  const int64_t dst_row = map.row_offset(b, hk, pos);
+  if (dst_row < 0) return;
+
+  const int64_t src = row * map.D + chunk * 8;
+  const int64_t dst = dst_row + chunk * 8;
+  const u32x4 kv = *reinterpret_cast<const u32x4*>(k_new + src);
+  const u32x4 vv = *reinterpret_cast<const u32x4*>(v_new + src);
+  *reinterpret_cast<u32x4*>(k_pages + dst) = kv;
+  *reinterpret_cast<u32x4*>(v_pages + dst) = vv;
+}
+
+hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
+                               const KVMap& map, int B, int Hk, int T, int start_pos,
+                               const int32_t* start_positions, hipStream_t stream) {
+  const int chunks_per_row = map.D / 8;
+  int chunk_shift = 0;
+  while ((1 << chunk_shift) < chunks_per_row) ++chunk_shift;
+  if ((1 << chunk_shift) != chunks_per_row) chunk_shift = -1;
+  const int64_t total = (int64_t)B * Hk * T * chunks_per_row;
+  if (total == 0) return hipSuccess;
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  hipLaunchKernelGGL(paged_append_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
+                     reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
+                     reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new), map,
+                     B, Hk, T, chunks_per_row, chunk_shift, start_pos, start_positions, total);
+  return hipGetLastError();
+}
+
+}  // namespace fa

@@ -1,0 +1,125 @@
+// Shared definitions of the gfx950 attention kernels: vector types, the page
+// map (logical page -> physical page -> element offset), and the launcher
+// prototypes the C-ABI layer (fa_abi.hip) dispatches to.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 f16;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Where the K/V rows of one (sequence, KV head) live.
+//
+// Contiguous K/V [B, Hk, N, D]: row j of (b, hk) is at ((b*Hk + hk)*N + j)*D.
+// Paged K/V [NB, Hk, P, PS, D]: logical page p = j / PS of sequence b maps to
+// a physical id phi (identity b*P + p, or block_table[b*max_blocks + p]), and
+// the row sits at (((phi/P)*Hk + hk)*P + phi%P)*PS*D + (j%PS)*D. The map follows
+// the reference's PagedAccessor (csrc/flash_attn_sm75.cu:54-86) with the block
+// table as an additive indirection.
+struct KVMap {
+  const int32_t* block_table;  // nullable
+  int64_t stride_nb;           // Hk*P*PS*D (paged) ; Hk*N*D (contiguous)
+  int64_t stride_hk;           // P*PS*D           ; N*D
+  int64_t stride_page;         // PS*D             ; unused
+  int max_blocks;              // logical pages per sequence (P without table)
+  int P;                       // pages per row of the pool
+  int num_phys;                // NB*P: valid physical ids are [0, num_phys)
+  int PS;                      // tokens per page
+  int ps_shift;                // log2(PS) when PS is a power of two, else -1
+  int D;
+  int paged;                   // 0: contiguous K/V
+
+  // Element offset of row j of (b, hk); -1 when the row is not addressable
+  // (page beyond the capacity or an out-of-range physical id).
+  __device__ __forceinline__ int64_t row_offset(int b, int hk, int j) const {
+    if (!paged) return (int64_t)b * stride_nb + (int64_t)hk * stride_hk + (int64_t)j * D;
+    int page, slot;
+    if (ps_shift >= 0) {
+      page = j >> ps_shift;
+      slot = j & (PS - 1);
+    } else {
+      page = j / PS;
+      slot = j - page * PS;
+    }
+    if (page >= max_blocks) return -1;
+    int phi;
+    if (block_table != nullptr) {
+      phi = block_table[(int64_t)b * max_blocks + page];
+      if (phi < 0 || phi >= num_phys) return -1;
+    } else {
+      phi = b * P + page;
+    }
+    int nb = phi / P;
+    int pp = phi - nb * P;
+    return (int64_t)nb * stride_nb + (int64_t)hk * stride_hk + (int64_t)pp * stride_page +
+           (int64_t)slot * D;
+  }
+};
+
+// Per-call arguments of the attention kernels (both contiguous and paged).
+struct AttnParams {
+  const void* q;      // [B, Hq, M, D]
+  const void* k;      // contiguous [B, Hk, N, D] or pool [NB, Hk, P, PS, D]
+  const void* v;
+  void* o;            // [B, Hq, M, D]
+  const int32_t* seqlen;    // paged: [B]; contiguous: nullptr (all N)
+  const int32_t* head_map;  // paged: [Hq]; contiguous: nullptr (h / group)
+  const int32_t* q_offsets; // nullable [B]
+  const int32_t* k_offsets; // nullable [B]
+  KVMap kv;
+  int B, Hq, Hk, M, N;  // N: contiguous key count, or per-sequence capacity in tokens
+  int group;            // Hq / Hk (contiguous head mapping)
+  int causal;
+  int q_offset, k_offset;
+  float scale_log2;     // log2(e) / sqrt(D)
+  // split-K decode scratch
+  float* ws_o;          // [B, Hq, M, nsplit, D]
+  float* ws_ml;         // [B, Hq, M, nsplit, 2]
+  int nsplit;
+  int split_tokens;
+
+  __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
+  __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
+  // Number of keys of sequence b (clamped to the capacity).
+  __device__ __forceinline__ int kv_len(int b) const {
+    if (seqlen == nullptr) return N;
+    int n = seqlen[b];
+    n = n < 0 ? 0 : n;
+    return n > N ? N : n;
+  }
+  // K/V head of query head hq, or -1 if the head map points outside [0, Hk).
+  __device__ __forceinline__ int kv_head(int hq) const {
+    if (head_map == nullptr) return hq / group;
+    int hk = head_map[hq];
+    return (hk >= 0 && hk < Hk) ? hk : -1;
+  }
+};
+
+// Launchers (return hipSuccess or the launch error).
+hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
+                               const KVMap& map, int B, int Hk, int T, int start_pos,
+                               const int32_t* start_positions, hipStream_t stream);
+hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream);
+hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
+
+// Split-K sizing of the decode path (host side; depends on sizes only).
+struct DecodePlan {
+  int nsplit;
+  int split_tokens;
+  size_t ws_bytes;
+};
+DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
+bool use_decode_path(int M, int Hq, int Hk);
+
+}  // namespace fa

@@ -1,0 +1,411 @@
+// Paged-KV decode attention for gfx950 (few query rows per head, long context).
+//
+// Semantics: the reference's flash_attn_paged with M small (decode: M == 1,
+// causal=False; engine/llama_tp.py:186-200), i.e. for query row (b, hq, i)
+//   o = softmax_j(q . k_j / sqrt(D)) v_j over keys j < seqlen[b]
+// (and k_off + j <= q_off + i when causal), with K/V of head head_map[hq]
+// (flashattention_custom/ops.py:37-63, csrc/flash_attn_sm75.cu:213-425).
+//
+// Design (HBM-bound; every K/V byte is read once per KV head):
+//  * One workgroup = (split of the context, KV head hk, sequence b). It serves
+//    every query row that reads hk: all q heads of the GQA group times the M
+//    query positions, packed as the 16 columns of the MFMA tiles. K/V pages are
+//    therefore read once per KV head, not once per query head.
+//  * The split's tokens are walked in 16-token groups; the 4 waves take groups
+//    round-robin and keep their own running (max, sum, O) state; the next
+//    group's K/V are loaded into registers before the current one is used.
+//  * S^T = K Q^T with v_mfma_f32_16x16x32_f16: lane (n, quarter) loads K row
+//    n of the group as 16-byte vectors straight from HBM (no LDS). The
+//    accumulator gives each lane 4 tokens of one query row, which is exactly
+//    the B-operand layout of the P^T side of O^T = V^T P^T
+//    (v_mfma_f32_16x16x16f16), so the softmax stays in registers.
+//  * V^T needs 4 tokens of one d per lane. Each lane loads 4 token rows, D/16
+//    consecutive d each (whole 256-byte rows across a quarter-wave), and the
+//    d index of the MFMA output is relabelled d = (D/16)*m + j so that the
+//    transpose is a byte permute inside the lane.
+//  * Partial (max, sum, O) of each split go to a workspace; a combine kernel
+//    merges the splits of a row in log2 space.
+#include "fa_common.h"
+
+#include <stdlib.h>
+
+namespace fa {
+
+namespace {
+
+constexpr int kDecodeThreads = 256;  // 4 waves
+constexpr int kDecodeWaves = 4;
+constexpr int kRows = 16;            // query rows per MFMA column block
+constexpr int kMaxHeads = 256;       // q heads scanned per KV head
+
+__device__ __forceinline__ float wave_max16x(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum16x(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Byte permute: (low half of x, low half of y) and (high half of x, high half of y).
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+template <int D>
+struct DecodeRegs {
+  static constexpr int KSTEPS = D / 32;  // 16x16x32 MFMAs for S^T
+  static constexpr int DPL = D / 16;     // d values per lane and token for V^T
+  static constexpr int VW = DPL / 2;     // dwords per V row fragment
+  u32x4 k[KSTEPS];
+  uint32_t v[4][VW];
+};
+
+// Loads the K/V fragments of one 16-token group (rows beyond `t_end` or not
+// addressable read as zero, so masked keys never carry NaN garbage into P V).
+template <int D>
+__device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p, const f16* kp,
+                                           const f16* vp, int b, int hk, int t0, int t_end,
+                                           int n, int quarter) {
+  constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
+  constexpr int DPL = DecodeRegs<D>::DPL;
+  constexpr int VW = DecodeRegs<D>::VW;
+  {
+    const int row = t0 + n;
+    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      if (off >= 0) {
+        r.k[kk] = *reinterpret_cast<const u32x4*>(kp + off + 32 * kk + 8 * quarter);
+      } else {
+        r.k[kk] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = t0 + 4 * quarter + i;
+    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
+    if constexpr (VW == 4) {
+      u32x4 x = u32x4{0u, 0u, 0u, 0u};
+      if (off >= 0) x = *reinterpret_cast<const u32x4*>(vp + off + DPL * n);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) r.v[i][w] = x[w];
+    } else {
+      u32x2 x = u32x2{0u, 0u};
+      if (off >= 0) x = *reinterpret_cast<const u32x2*>(vp + off + DPL * n);
+#pragma unroll
+      for (int w = 0; w < VW; ++w) r.v[i][w] = x[w];
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams p) {
+  constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
+  constexpr int DPL = DecodeRegs<D>::DPL;
+  constexpr int VW = DecodeRegs<D>::VW;
+  constexpr int OPAD = D + 4;
+
+  __shared__ int s_heads[kMaxHeads];
+  __shared__ int s_count;
+  __shared__ float s_m[kDecodeWaves][kRows];
+  __shared__ float s_l[kDecodeWaves][kRows];
+  __shared__ float s_o[kDecodeWaves][kRows][OPAD];
+
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15;       // MFMA column: query row within the block
+  const int quarter = lane >> 4; // 0..3
+
+  const int kv_len = p.kv_len(b);
+  const int qo = p.q_off(b);
+  const int ko = p.k_off(b);
+  int kv_lim = kv_len;
+  if (p.causal) {
+    int64_t lim = (int64_t)qo + (p.M - 1) - ko + 1;
+    if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
+  }
+  const int t_begin = split * p.split_tokens;
+  if (t_begin >= kv_lim) return;  // the combine kernel skips this split
+  const int t_end = min(kv_lim, t_begin + p.split_tokens);
+
+  // Query heads that read KV head hk (any head_map, not only h / group).
+  if (wave == 0) {
+    int count = 0;
+    for (int base = 0; base < p.Hq; base += 64) {
+      const int hq = base + lane;
+      const bool match = hq < p.Hq && p.kv_head(hq) == hk;
+      const uint64_t mask = __ballot(match);
+      if (match) {
+        const int pos = count + __popcll(mask & ((1ull << lane) - 1ull));
+        if (pos < kMaxHeads) s_heads[pos] = hq;
+      }
+      count += __popcll(mask);
+    }
+    if (lane == 0) s_count = min(count, kMaxHeads);
+  }
+  __syncthreads();
+  const int nrows = s_count * p.M;
+
+  const f16* qp = reinterpret_cast<const f16*>(p.q);
+  const f16* kp = reinterpret_cast<const f16*>(p.k);
+  const f16* vp = reinterpret_cast<const f16*>(p.v);
+  const float c = p.scale_log2;
+
+  const int g_begin = t_begin >> 4;
+  const int g_end = (t_end + 15) >> 4;
+
+  for (int rc = 0; rc < nrows; rc += kRows) {
+    // This lane's query row (column n of the tiles).
+    const int ridx = rc + n;
+    const bool row_ok = ridx < nrows;
+    const int hq = row_ok ? s_heads[ridx / p.M] : 0;
+    const int qi = row_ok ? ridx % p.M : 0;
+    int row_lim = t_end;  // keys j < row_lim are visible to this row
+    if (p.causal) {
+      int64_t lim = (int64_t)qo + qi - ko + 1;
+      if (lim < row_lim) row_lim = lim < 0 ? 0 : (int)lim;
+    }
+
+    half8 qreg[KSTEPS];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      if (row_ok) {
+        const int64_t qoff = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 32 * kk + 8 * quarter;
+        qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
+      } else {
+        qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+    floatx4 acc_o[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    int g = g_begin + wave;
+    DecodeRegs<D> cur;
+    if (g < g_end) load_group<D>(cur, p, kp, vp, b, hk, g << 4, t_end, n, quarter);
+    while (g < g_end) {
+      const int t0 = g << 4;
+      const int g_next = g + kDecodeWaves;
+      DecodeRegs<D> nxt;
+      if (g_next < g_end) load_group<D>(nxt, p, kp, vp, b, hk, g_next << 4, t_end, n, quarter);
+
+      // S^T[token][row] for the 16 tokens of the group.
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, cur.k[kk]), qreg[kk],
+                                                   s, 0, 0, 0);
+      }
+      // lane holds tokens t0 + 4*quarter + r of row n
+      float sv[4];
+      float gmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = t0 + 4 * quarter + r;
+        sv[r] = tok < row_lim ? s[r] : -INFINITY;
+        gmax = fmaxf(gmax, sv[r]);
+      }
+      gmax = wave_max16x(gmax);
+      const float m_new = fmaxf(m_run, gmax);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
+      const float mc = m_use * c;
+      float pr[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], c, -mc));
+        psum += pr[r];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      const half4 pb = half4{(f16)pr[0], (f16)pr[1], (f16)pr[2], (f16)pr[3]};
+
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const int w = j >> 1;
+        uint32_t lo, hi;
+        if ((j & 1) == 0) {
+          lo = pack_lo(cur.v[0][w], cur.v[1][w]);
+          hi = pack_lo(cur.v[2][w], cur.v[3][w]);
+        } else {
+          lo = pack_hi(cur.v[0][w], cur.v[1][w]);
+          hi = pack_hi(cur.v[2][w], cur.v[3][w]);
+        }
+        const half4 a = __builtin_bit_cast(half4, u32x2{lo, hi});
+        acc_o[j] = acc_o[j] * alpha;
+        acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc_o[j], 0, 0, 0);
+      }
+      (void)VW;
+      cur = nxt;
+      g = g_next;
+    }
+
+    // Merge the 4 waves' states in LDS: m is uniform per row, l needs the
+    // 4 lanes of a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j.
+    l_run = wave_sum16x(l_run);
+    if (quarter == 0) {
+      s_m[wave][n] = m_run;
+      s_l[wave][n] = l_run;
+    }
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_o[wave][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
+    }
+    __syncthreads();
+
+    for (int e = tid; e < kRows * D; e += kDecodeThreads) {
+      const int row = e / D;
+      const int d = e - row * D;
+      const int ri = rc + row;
+      if (ri >= nrows) continue;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][row]);
+      float lsum = 0.f, osum = 0.f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          const float sc = __builtin_amdgcn_exp2f((s_m[w][row] - mx) * c);
+          lsum += sc * s_l[w][row];
+          osum += sc * s_o[w][row][d];
+        }
+      }
+      const int rhq = s_heads[ri / p.M];
+      const int rqi = ri % p.M;
+      const int64_t slot = (((int64_t)b * p.Hq + rhq) * p.M + rqi) * p.nsplit + split;
+      p.ws_o[slot * D + d] = osum;
+      if (d == 0) {
+        p.ws_ml[slot * 2 + 0] = mx;
+        p.ws_ml[slot * 2 + 1] = lsum;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Merges the split partials of one query row: one wave per (b, hq, i).
+template <int D>
+__global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
+  constexpr int DPW = D / 64;  // d values per lane
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int total = p.B * p.Hq * p.M;
+  if (row >= total) return;
+  const int qi = row % p.M;
+  const int hq = (row / p.M) % p.Hq;
+  const int b = row / (p.M * p.Hq);
+  f16* op = reinterpret_cast<f16*>(p.o) + (int64_t)row * D;
+
+  const int kv_len = p.kv_len(b);
+  int kv_lim = kv_len;
+  if (p.causal) {
+    int64_t lim = (int64_t)p.q_off(b) + (p.M - 1) - p.k_off(b) + 1;
+    if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
+  }
+  const int nsp = kv_lim > 0 ? (kv_lim + p.split_tokens - 1) / p.split_tokens : 0;
+  const bool head_ok = p.kv_head(hq) >= 0;
+
+  float result[DPW];
+  if (!head_ok) {
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) result[k] = __builtin_nanf("");
+  } else if (kv_len == 0) {
+    // Zero keys: softmax over an empty row times an empty V is zero
+    // (flashattention_custom/ops.py:55-62 with slen == 0).
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) result[k] = 0.f;
+  } else {
+    const int64_t slot0 = (int64_t)row * p.nsplit;
+    float mx = -INFINITY;
+    for (int s = 0; s < nsp; ++s) mx = fmaxf(mx, p.ws_ml[(slot0 + s) * 2]);
+    float lsum = 0.f;
+    float acc[DPW];
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
+    if (mx != -INFINITY) {
+      const float c = p.scale_log2;
+      for (int s = 0; s < nsp; ++s) {
+        const float sc = __builtin_amdgcn_exp2f((p.ws_ml[(slot0 + s) * 2] - mx) * c);
+        lsum += sc * p.ws_ml[(slot0 + s) * 2 + 1];
+#pragma unroll
+        for (int k = 0; k < DPW; ++k) acc[k] += sc * p.ws_o[(slot0 + s) * D + lane + 64 * k];
+      }
+    }
+    // No visible key (lsum == 0): 0 * inf = NaN, the reference's result for a
+    // fully masked row.
+    const float inv = 1.f / lsum;
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) result[k] = acc[k] * inv;
+  }
+#pragma unroll
+  for (int k = 0; k < DPW; ++k) op[lane + 64 * k] = (f16)result[k];
+}
+
+int env_split_tokens() {
+  static int cached = -2;
+  if (cached == -2) {
+    const char* s = getenv("FA_DECODE_SPLIT_TOKENS");
+    int v = s ? atoi(s) : 0;
+    cached = (v >= 64) ? ((v + 63) / 64) * 64 : -1;
+  }
+  return cached;
+}
+
+}  // namespace
+
+bool use_decode_path(int M, int Hq, int Hk) {
+  if (Hk <= 0 || Hq > kMaxHeads) return false;
+  const int group = (Hq + Hk - 1) / Hk;
+  return M >= 1 && (int64_t)M * group <= 4 * kRows;
+}
+
+DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens) {
+  DecodePlan plan;
+  int split = env_split_tokens();
+  if (split < 0) split = 1024;
+  if (capacity_tokens < 1) capacity_tokens = 1;
+  plan.split_tokens = split;
+  plan.nsplit = (capacity_tokens + split - 1) / split;
+  const size_t slots = (size_t)B * Hq * M * plan.nsplit;
+  const size_t o_bytes = ((slots * D * sizeof(float)) + 255) / 256 * 256;
+  plan.ws_bytes = o_bytes + slots * 2 * sizeof(float);
+  (void)Hk;
+  return plan;
+}
+
+hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
+  const dim3 grid((unsigned)p.nsplit, (unsigned)p.Hk, (unsigned)p.B);
+  const int rows = p.B * p.Hq * p.M;
+  const dim3 cgrid((unsigned)((rows + 3) / 4));
+  if (D == 128) {
+    hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(kDecodeThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(kDecodeThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(256), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fa

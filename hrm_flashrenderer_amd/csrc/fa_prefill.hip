@@ -1,0 +1,384 @@
+// Causal / non-causal flash-attention prefill for gfx950 (contiguous or paged
+// K/V, MHA or GQA), and an fp32 variant of the contiguous op.
+//
+// Semantics: the reference's flash_attn / flash_attn_paged
+// (flashattention_custom/ops.py:22-63, csrc/flash_attn_sm75.cu:89-425):
+//   O[b,h,i] = sum_j softmax_j(Q[b,h,i] . K[b,hk,j] / sqrt(D)) V[b,hk,j]
+// over keys j < N_b with k_off + j <= q_off + i when causal.
+//
+// fp16 kernel design (MFMA-bound):
+//  * Workgroup = 128 query rows of one (b, hq): 4 waves x 32 rows. Q stays in
+//    registers as the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_f16).
+//  * K/V stream through LDS in 64-key tiles. The next tile's rows are fetched
+//    from HBM into registers while the current tile is computed. K is stored
+//    row-major (padded rows); V is stored transposed (Vt[d][key], padded) by
+//    a byte permute in registers, so that the A operand of O^T = V^T P^T is
+//    two 8-byte LDS reads per MFMA.
+//  * Both products keep the query row as the MFMA column: every lane owns one
+//    query row, the softmax max/sum is an in-lane reduction plus one exchange
+//    with lane ^ 32, and the rescale of O^T by exp(m_old - m_new) is a single
+//    per-lane factor. P never leaves registers: the S^T accumulator registers
+//    are already in the B-operand layout of the P^T side (with the key order
+//    inside a 16-key step permuted identically on the V^T side).
+//  * Causal tiles beyond the diagonal are never loaded; waves whose rows see
+//    none of a tile skip its math; the q-tile order is reversed so the longest
+//    rows start first.
+#include "fa_common.h"
+
+namespace fa {
+
+namespace {
+
+constexpr int kBM = 128;     // query rows per workgroup
+constexpr int kBN = 64;      // keys per tile
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Key limit of one query row: keys j < limit are visible.
+__device__ __forceinline__ int row_key_limit(int kv_len, int causal, int qo, int ko, int row) {
+  int lim = kv_len;
+  if (causal) {
+    const int64_t c = (int64_t)qo + row - ko + 1;
+    if (c < lim) lim = c < 0 ? 0 : (int)c;
+  }
+  return lim;
+}
+
+template <int D>
+struct TileRegs {
+  static constexpr int KCH = kBN * D / 8 / kThreads;   // 16-byte K chunks per thread
+  static constexpr int KPT = kBN * D / 8 / kThreads;   // keys per thread for V (x 8 d)
+  u32x4 k[KCH];
+  u32x4 v[KPT];
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, const AttnParams& p, const f16* kp,
+                                          const f16* vp, int b, int hk, int k0, int kv_len,
+                                          int tid) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int KCH = TileRegs<D>::KCH;
+  constexpr int KPT = TileRegs<D>::KPT;
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / CPR;
+    const int col = c % CPR;
+    const int j = k0 + row;
+    const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
+    r.k[i] = off >= 0 ? *reinterpret_cast<const u32x4*>(kp + off + 8 * col)
+                      : u32x4{0u, 0u, 0u, 0u};
+  }
+  {
+    const int kg = tid / CPR;  // key group: keys KPT*kg .. +KPT
+    const int dc = tid % CPR;  // d chunk: d = 8*dc .. +8
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int j = k0 + KPT * kg + i;
+      const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
+      r.v[i] = off >= 0 ? *reinterpret_cast<const u32x4*>(vp + off + 8 * dc)
+                        : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void store_tile(const TileRegs<D>& r, f16* sK, f16* sVt, int tid) {
+  constexpr int CPR = D / 8;
+  constexpr int KPAD = D + 8;
+  constexpr int VPAD = kBN + 8;
+  constexpr int KCH = TileRegs<D>::KCH;
+  constexpr int KPT = TileRegs<D>::KPT;
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / CPR;
+    const int col = c % CPR;
+    *reinterpret_cast<u32x4*>(sK + row * KPAD + 8 * col) = r.k[i];
+  }
+  const int kg = tid / CPR;
+  const int dc = tid % CPR;
+  // Transpose KPT keys x 8 d into 8 rows of Vt holding KPT consecutive keys.
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    if constexpr (KPT == 4) {
+      const u32x2 lo = u32x2{pack_lo(r.v[0][w], r.v[1][w]), pack_lo(r.v[2][w], r.v[3][w])};
+      const u32x2 hi = u32x2{pack_hi(r.v[0][w], r.v[1][w]), pack_hi(r.v[2][w], r.v[3][w])};
+      *reinterpret_cast<u32x2*>(sVt + (8 * dc + 2 * w) * VPAD + KPT * kg) = lo;
+      *reinterpret_cast<u32x2*>(sVt + (8 * dc + 2 * w + 1) * VPAD + KPT * kg) = hi;
+    } else {
+      *reinterpret_cast<uint32_t*>(sVt + (8 * dc + 2 * w) * VPAD + KPT * kg) =
+          pack_lo(r.v[0][w], r.v[1][w]);
+      *reinterpret_cast<uint32_t*>(sVt + (8 * dc + 2 * w + 1) * VPAD + KPT * kg) =
+          pack_hi(r.v[0][w], r.v[1][w]);
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
+  constexpr int KSTEPS = D / 16;  // k-steps of S^T
+  constexpr int DBLK = D / 32;    // 32-row blocks of O^T
+  constexpr int KPAD = D + 8;
+  constexpr int VPAD = kBN + 8;
+  __shared__ __attribute__((aligned(16))) f16 sK[kBN * KPAD];
+  __shared__ __attribute__((aligned(16))) f16 sVt[D * VPAD];
+
+  const int qt = gridDim.x - 1 - blockIdx.x;
+  const int hq = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31;   // query row within the wave
+  const int half_id = lane >> 5;
+
+  const int q0 = qt * kBM;
+  const int qrow = q0 + wave * 32 + col;
+  f16* op = reinterpret_cast<f16*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
+
+  const int hk = p.kv_head(hq);
+  if (hk < 0) {
+    if (qrow < p.M) {
+      for (int d = half_id * (D / 2); d < (half_id + 1) * (D / 2); ++d)
+        op[(int64_t)qrow * D + d] = (f16)__builtin_nanf("");
+    }
+    return;
+  }
+
+  const int kv_len = p.kv_len(b);
+  const int qo = p.q_off(b);
+  const int ko = p.k_off(b);
+  const int last_row = min(q0 + kBM, p.M) - 1;
+  const int wg_lim = row_key_limit(kv_len, p.causal, qo, ko, last_row);
+  const int ntiles = (wg_lim + kBN - 1) / kBN;
+
+  const int wrow0 = q0 + wave * 32;
+  const int wrow1 = min(wrow0 + 31, p.M - 1);
+  const bool wave_rows = wrow0 < p.M;
+  const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
+  const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
+  const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
+
+  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const f16* kp = reinterpret_cast<const f16*>(p.k);
+  const f16* vp = reinterpret_cast<const f16*>(p.v);
+
+  half8 qreg[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    qreg[ks] = qrow < p.M
+                   ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
+                   : half8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  floatx16 acc_o[DBLK];
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) acc_o[i] = floatx16{};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  const float c = p.scale_log2;
+
+  TileRegs<D> regs;
+  if (ntiles > 0) load_tile<D>(regs, p, kp, vp, b, hk, 0, kv_len, tid);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = t * kBN;
+    __syncthreads();
+    store_tile<D>(regs, sK, sVt, tid);
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile<D>(regs, p, kp, vp, b, hk, k0 + kBN, kv_len, tid);
+    if (k0 >= wave_lim_max) continue;
+
+    // S^T[key][row]: two 32-key blocks.
+    floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const half8 a0 = *reinterpret_cast<const half8*>(sK + col * KPAD + 16 * ks + 8 * half_id);
+      const half8 a1 =
+          *reinterpret_cast<const half8*>(sK + (32 + col) * KPAD + 16 * ks + 8 * half_id);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
+    }
+    // Register r of block mb holds key k0 + 32*mb + 8*(r/4) + 4*half_id + r%4.
+    if (k0 + kBN > wave_lim_min) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * half_id + (r & 3);
+        if (key >= lim) s0[r] = -INFINITY;
+        if (key + 32 >= lim) s1[r] = -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
+    const float mc = m_use * c;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -mc));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -mc));
+      psum += s0[r] + s1[r];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < DBLK; ++i) acc_o[i] = acc_o[i] * alpha;
+
+    // P^T operands of the four 16-key steps.
+    half8 pb[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pb[0][j] = (f16)s0[j];
+      pb[1][j] = (f16)s0[8 + j];
+      pb[2][j] = (f16)s1[j];
+      pb[3][j] = (f16)s1[8 + j];
+    }
+    // O^T[d][row] += V^T[d][key] P^T[key][row]; within step s the lane's k
+    // slot j maps to key 16*s + 8*(j/4) + 4*half_id + j%4.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i) {
+        const f16* vrow = sVt + (32 * i + col) * VPAD + 16 * s + 4 * half_id;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+        const half8 a = __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[s], acc_o[i], 0, 0, 0);
+      }
+    }
+  }
+
+  if (qrow >= p.M) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  // kv_len == 0: zeros (empty softmax times empty V); otherwise a row without
+  // visible keys gives 0 * inf = NaN, as the reference does.
+  const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
+  f16* orow = op + (int64_t)qrow * D;
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
+                            (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      *reinterpret_cast<half4*>(orow + 32 * i + 8 * g + 4 * half_id) = h;
+    }
+  }
+}
+
+// fp32 contiguous attention (the reference's CPU path accepts fp32,
+// flashattention_custom/ops.py:22-34). Exact fp32 arithmetic on the vector
+// ALUs: one wave of 64 query rows per workgroup, Q rows in LDS, K/V streamed
+// in 16-key tiles.
+template <int D>
+__global__ __launch_bounds__(64) void prefill_f32_kernel(AttnParams p) {
+  constexpr int BN = 16;
+  __shared__ float sQ[64][D + 1];
+  __shared__ float sK[BN][D];
+  __shared__ float sV[BN][D];
+  const int qt = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int q0 = qt * 64;
+  const int qrow = q0 + lane;
+  float* op = reinterpret_cast<float*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const float* qp = reinterpret_cast<const float*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const float* kp = reinterpret_cast<const float*>(p.k);
+  const float* vp = reinterpret_cast<const float*>(p.v);
+  const int hk = p.kv_head(hq);
+  const int kv_len = p.kv_len(b);
+  const int qo = p.q_off(b);
+  const int ko = p.k_off(b);
+
+  for (int e = lane; e < 64 * D; e += 64) {
+    const int r = e / D, d = e % D;
+    sQ[r][d] = (q0 + r < p.M) ? qp[(int64_t)(q0 + r) * D + d] : 0.f;
+  }
+  const int last_row = min(q0 + 64, p.M) - 1;
+  const int wg_lim = hk < 0 ? 0 : row_key_limit(kv_len, p.causal, qo, ko, last_row);
+  const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
+  const float scale = p.scale_log2 / kLog2e;  // 1/sqrt(D)
+
+  float o[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) o[d] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  for (int k0 = 0; k0 < wg_lim; k0 += BN) {
+    __syncthreads();
+    for (int e = lane; e < BN * D; e += 64) {
+      const int r = e / D, d = e % D;
+      const int j = k0 + r;
+      const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
+      sK[r][d] = off >= 0 ? kp[off + d] : 0.f;
+      sV[r][d] = off >= 0 ? vp[off + d] : 0.f;
+    }
+    __syncthreads();
+    float s[BN];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < BN; ++r) {
+      float acc = 0.f;
+#pragma unroll 16
+      for (int d = 0; d < D; ++d) acc = __builtin_fmaf(sQ[lane][d], sK[r][d], acc);
+      s[r] = (k0 + r < lim) ? acc * scale : -INFINITY;
+      mx = fmaxf(mx, s[r]);
+    }
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = expf(m_run - m_use);
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < BN; ++r) {
+      s[r] = expf(s[r] - m_use);
+      psum += s[r];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      float acc = o[d] * alpha;
+#pragma unroll
+      for (int r = 0; r < BN; ++r) acc = __builtin_fmaf(s[r], sV[r][d], acc);
+      o[d] = acc;
+    }
+  }
+  if (qrow >= p.M) return;
+  float inv;
+  if (hk < 0) inv = __builtin_nanf("");
+  else inv = kv_len == 0 ? 0.f : 1.f / l_run;
+#pragma unroll
+  for (int d = 0; d < D; ++d) op[(int64_t)qrow * D + d] = o[d] * inv;
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream) {
+  if (dtype == 1) {
+    const dim3 grid((unsigned)((p.M + 63) / 64), (unsigned)p.Hq, (unsigned)p.B);
+    if (D == 128)
+      hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(64), 0, stream, p);
+    else
+      hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(64), 0, stream, p);
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)((p.M + kBM - 1) / kBM), (unsigned)p.Hq, (unsigned)p.B);
+  if (D == 128)
+    hipLaunchKernelGGL(prefill_f16_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(prefill_f16_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace fa

@@ -1,0 +1,305 @@
+"""Operator API of the MI355X attention path — drop-in for `flashattention_custom.ops`.
+
+Public functions (same names, positional order, defaults and return
+conventions as the reference, flashattention_custom/ops.py:79-99):
+
+  flash_attn(q, k, v, causal=True, q_offset=0, k_offset=0) -> Tensor
+  flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
+                   causal=True, q_offset=0, k_offset=0, *, block_table=None) -> Tensor
+  paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
+                  *, block_table=None) -> None
+
+Each validates its arguments in Python with the reference extension's
+messages (csrc/ext.cpp:30-89), then calls a `torch.library` custom op
+(`hrm_fa::*`) whose body calls the C ABI of libfa_mi355x.so on the current
+stream of the tensors' device. There is no CPU fallback: tensors must be on a
+ROCm device and the library must be built, otherwise a RuntimeError is raised
+(the reference's `_ext` raises the same "CUDA required" checks; the wording
+refers to torch's device type, which is "cuda" on ROCm).
+
+Additive, keyword-compatible extensions (defaults give the reference
+behaviour):
+  * `q_offset` / `k_offset` / `start_pos` accept an int32 device tensor [B]
+    of per-sequence values besides a Python int.
+  * `block_table` (int32 [B, max_blocks]): logical page p of sequence b is
+    physical page phi = block_table[b, p] of the pool, i.e.
+    k_pages[phi // P, :, phi % P]. With it, k_pages.size(0) need not be B.
+  * `flash_attn` also accepts fp32 q/k/v (fp32 arithmetic) and GQA
+    (k.size(1) dividing q.size(1); q head h reads K/V head h // (Hq // Hk)).
+"""
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import torch
+
+from . import _lib
+
+IntOrTensor = Union[int, torch.Tensor]
+
+_HEAD_DIMS = (64, 128)
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _device_index(t: torch.Tensor) -> int:
+    return t.device.index if t.device.index is not None else torch.cuda.current_device()
+
+
+class _DeviceScope:
+    """Makes the tensors' device current for the duration of a library call."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = _device_index(t)
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+        return torch.cuda.current_stream(self.idx).cuda_stream
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _per_seq(value: IntOrTensor, B: int, name: str, device: torch.device,
+             require_device: bool = True):
+    """Split a scalar-or-tensor offset into (int scalar, optional int32 [B] tensor)."""
+    if isinstance(value, torch.Tensor):
+        if value.dim() == 0:
+            return int(value.item()), None
+        if require_device:
+            _check(value.is_cuda, f"{name} tensor must be CUDA")
+        _check(value.device == device, f"{name} tensor must be on the q device")
+        _check(value.dtype == torch.int32, f"{name} int32 required")
+        _check(value.is_contiguous(), "contiguous required")
+        _check(value.dim() == 1 and value.numel() == B, f"{name} [B] required")
+        return 0, value
+    return int(value), None
+
+
+def _check_block_table(block_table: Optional[torch.Tensor], B: int, device: torch.device,
+                       require_device: bool = True) -> int:
+    if block_table is None:
+        return 0
+    if require_device:
+        _check(block_table.is_cuda, "CUDA required")
+    _check(block_table.device == device, "tensors must be on one device")
+    _check(block_table.dtype == torch.int32, "block_table int32 required")
+    _check(block_table.is_contiguous(), "contiguous required")
+    _check(block_table.dim() == 2 and block_table.size(0) == B, "block_table [B, max_blocks] required")
+    return int(block_table.size(1))
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# --------------------------------------------------------------------------
+# custom ops (bodies call the C ABI; fake impls make them traceable)
+# --------------------------------------------------------------------------
+
+@torch.library.custom_op("hrm_fa::flash_attn", mutates_args=())
+def _flash_attn_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool,
+                   q_offset: int, k_offset: int, q_offsets: Optional[torch.Tensor],
+                   k_offsets: Optional[torch.Tensor]) -> torch.Tensor:
+    lib = _lib.load()
+    o = torch.empty_like(q)
+    B, Hq, M, D = q.shape
+    Hk, N = k.size(1), k.size(2)
+    dtype = _lib.FA_DTYPE_F16 if q.dtype == torch.float16 else _lib.FA_DTYPE_F32
+    with _DeviceScope(q) as stream:
+        _lib.check(lib.fa_flash_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
+            B, Hq, Hk, M, N, D, int(causal), q_offset, k_offset,
+            _ptr(q_offsets), _ptr(k_offsets), stream))
+    return o
+
+
+@_flash_attn_op.register_fake
+def _(q, k, v, causal, q_offset, k_offset, q_offsets, k_offsets):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("hrm_fa::flash_attn_paged", mutates_args=())
+def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                         seqlen: torch.Tensor, page_size: int, head_map: torch.Tensor,
+                         causal: bool, q_offset: int, k_offset: int,
+                         q_offsets: Optional[torch.Tensor], k_offsets: Optional[torch.Tensor],
+                         block_table: Optional[torch.Tensor]) -> torch.Tensor:
+    lib = _lib.load()
+    o = torch.empty_like(q)
+    B, Hq, M, D = q.shape
+    NB, Hk, P = k_pages.size(0), k_pages.size(1), k_pages.size(2)
+    max_blocks = int(block_table.size(1)) if block_table is not None else 0
+    cap_pages = max_blocks if block_table is not None else P
+    ws_bytes = lib.fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    with _DeviceScope(q) as stream:
+        _lib.check(lib.fa_flash_attn_paged_fwd(
+            q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(), page_size,
+            head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P, int(causal),
+            q_offset, k_offset, _ptr(q_offsets), _ptr(k_offsets), _ptr(block_table), max_blocks,
+            _ptr(ws), ws_bytes, stream))
+    return o
+
+
+@_flash_attn_paged_op.register_fake
+def _(q, k_pages, v_pages, seqlen, page_size, head_map, causal, q_offset, k_offset, q_offsets,
+      k_offsets, block_table):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("hrm_fa::paged_kv_append", mutates_args=("k_pages", "v_pages"))
+def _paged_kv_append_op(k_pages: torch.Tensor, v_pages: torch.Tensor, k_new: torch.Tensor,
+                        v_new: torch.Tensor, start_pos: int, start_positions: Optional[torch.Tensor],
+                        page_size: int, block_table: Optional[torch.Tensor]) -> None:
+    lib = _lib.load()
+    B, Hk, T, D = k_new.shape
+    NB, P = k_pages.size(0), k_pages.size(2)
+    max_blocks = int(block_table.size(1)) if block_table is not None else 0
+    with _DeviceScope(k_pages) as stream:
+        _lib.check(lib.fa_paged_kv_append(
+            k_pages.data_ptr(), v_pages.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+            B, Hk, T, D, NB, P, page_size, start_pos, _ptr(start_positions),
+            _ptr(block_table), max_blocks, stream))
+
+
+@_paged_kv_append_op.register_fake
+def _(k_pages, v_pages, k_new, v_new, start_pos, start_positions, page_size, block_table):
+    return None
+
+
+# --------------------------------------------------------------------------
+# public API
+# --------------------------------------------------------------------------
+
+def validate_flash_attn(q, k, v, require_device: bool = True) -> None:
+    """Argument checks of flash_attn, in the order of csrc/ext.cpp:31-38."""
+    if require_device:
+        _check(q.is_cuda and k.is_cuda and v.is_cuda, "q/k/v must be CUDA")
+    _check((q.dtype == k.dtype == v.dtype) and q.dtype in (torch.float16, torch.float32),
+           "fp16 required")
+    _check(q.is_contiguous() and k.is_contiguous() and v.is_contiguous(), "contiguous required")
+    _check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be 4D")
+    _check(q.size(0) == k.size(0) and q.size(0) == v.size(0), "B mismatch")
+    _check(k.size(1) == v.size(1) and k.size(1) > 0 and q.size(1) % k.size(1) == 0, "H mismatch")
+    _check(k.size(2) == v.size(2), "N mismatch")
+    _check(q.size(3) == k.size(3) and q.size(3) == v.size(3), "D mismatch")
+    _check(q.device == k.device == v.device, "q/k/v must be on one device")
+    _check(q.size(3) in _HEAD_DIMS, "Supported head_dim: 64 or 128")
+
+
+def flash_attn(q, k, v, causal=True, q_offset=0, k_offset=0):
+    """Contiguous attention O = softmax(Q K^T / sqrt(D), causal mask) V.
+
+    Reference: flashattention_custom/ops.py:82-85 -> csrc/ext.cpp:30-40.
+    q [B,Hq,M,D], k/v [B,Hk,N,D]; returns a new tensor shaped like q.
+    """
+    validate_flash_attn(q, k, v)
+    B = q.size(0)
+    qo, qo_t = _per_seq(q_offset, B, "q_offset", q.device)
+    ko, ko_t = _per_seq(k_offset, B, "k_offset", q.device)
+    return _flash_attn_op(q, k, v, bool(causal), qo, ko, qo_t, ko_t)
+
+
+def validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
+                              block_table=None, require_device: bool = True) -> int:
+    """Argument checks of flash_attn_paged (csrc/ext.cpp:53-66 order, then the
+    extensions); returns max_blocks of the block table (0 without one)."""
+    if require_device:
+        _check(q.is_cuda and k_pages.is_cuda and v_pages.is_cuda, "CUDA required")
+        _check(seqlen.is_cuda and head_map.is_cuda, "CUDA required")
+    _check(q.dtype == torch.float16 and k_pages.dtype == torch.float16
+           and v_pages.dtype == torch.float16, "fp16 required")
+    _check(seqlen.dtype == torch.int32, "seqlen int32 required")
+    _check(head_map.dtype == torch.int32, "head_map int32 required")
+    _check(q.is_contiguous() and k_pages.is_contiguous() and v_pages.is_contiguous(),
+           "contiguous required")
+    _check(seqlen.is_contiguous() and head_map.is_contiguous(), "contiguous required")
+    _check(q.dim() == 4, "q [B,Hq,M,D]")
+    _check(k_pages.dim() == 5 and v_pages.dim() == 5, "k_pages/v_pages [B,Hk,P,PS,D]")
+    _check(k_pages.shape == v_pages.shape, "k_pages/v_pages mismatch")
+    B = q.size(0)
+    _check(block_table is not None or q.size(0) == k_pages.size(0), "B mismatch")
+    _check(head_map.dim() == 1 and q.size(1) == head_map.size(0), "Hq mismatch")
+    _check(k_pages.size(3) == page_size, "page_size mismatch")
+    _check(k_pages.size(4) == q.size(3), "D mismatch")
+    _check(q.size(3) in _HEAD_DIMS, "Supported head_dim: 64 or 128")
+    _check(seqlen.dim() == 1 and seqlen.numel() >= B, "seqlen [B] required")
+    dev = q.device
+    _check(k_pages.device == dev and v_pages.device == dev and seqlen.device == dev
+           and head_map.device == dev, "tensors must be on one device")
+    return _check_block_table(block_table, B, dev, require_device)
+
+
+def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
+                     causal=True, q_offset=0, k_offset=0, *, block_table=None):
+    """Attention of q over paged K/V (prefill chunk or decode).
+
+    Reference: flashattention_custom/ops.py:88-95 -> csrc/ext.cpp:42-68.
+    q [B,Hq,M,D] fp16; k_pages/v_pages [NB,Hk,P,PS,D] fp16; seqlen int32 [B];
+    head_map int32 [Hq]. Returns a new tensor shaped like q.
+    """
+    page_size = int(page_size)
+    validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
+    B = q.size(0)
+    qo, qo_t = _per_seq(q_offset, B, "q_offset", q.device)
+    ko, ko_t = _per_seq(k_offset, B, "k_offset", q.device)
+    return _flash_attn_paged_op(q, k_pages, v_pages, seqlen, page_size, head_map, bool(causal),
+                                qo, ko, qo_t, ko_t, block_table)
+
+
+def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
+                             block_table=None, require_device: bool = True):
+    """Argument checks of paged_kv_append (csrc/ext.cpp:78-87 order, then the
+    extensions); returns (scalar start, per-sequence start tensor or None)."""
+    if require_device:
+        _check(k_pages.is_cuda and v_pages.is_cuda and k_new.is_cuda and v_new.is_cuda,
+               "CUDA required")
+    _check(k_pages.dtype == torch.float16 and v_pages.dtype == torch.float16
+           and k_new.dtype == torch.float16 and v_new.dtype == torch.float16, "fp16 required")
+    _check(k_pages.is_contiguous() and v_pages.is_contiguous() and k_new.is_contiguous()
+           and v_new.is_contiguous(), "contiguous required")
+    _check(k_pages.dim() == 5 and k_new.dim() == 4, "shape mismatch")
+    _check(k_pages.shape == v_pages.shape, "k_pages/v_pages mismatch")
+    _check(k_new.shape == v_new.shape, "k_new/v_new mismatch")
+    B, Hk, T, D = k_new.shape
+    _check(block_table is not None or k_pages.size(0) == B, "B mismatch")
+    _check(k_pages.size(1) == Hk, "Hk mismatch")
+    _check(k_pages.size(3) == page_size, "page_size mismatch")
+    _check(k_pages.size(4) == D, "D mismatch")
+    _check(D % 8 == 0, "head_dim must be a multiple of 8")
+    dev = k_pages.device
+    _check(v_pages.device == dev and k_new.device == dev and v_new.device == dev,
+           "tensors must be on one device")
+    max_blocks = _check_block_table(block_table, B, dev, require_device)
+    sp, sp_t = _per_seq(start_pos, B, "start_pos", dev, require_device)
+    if sp_t is None and T > 0:
+        cap = (max_blocks if block_table is not None else k_pages.size(2)) * page_size
+        _check(sp >= 0 and sp + T <= cap,
+               f"start_pos {sp} + T {T} exceeds the page capacity {cap}")
+    return sp, sp_t
+
+
+def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, block_table=None):
+    """Write k_new/v_new [B,Hk,T,D] at positions start_pos + t of each sequence, in place.
+
+    Reference: flashattention_custom/ops.py:98-102 -> csrc/ext.cpp:70-89.
+    A Python-int start_pos is range-checked against the page capacity and
+    raises; per-sequence (tensor) starts skip out-of-range positions on the
+    device, as the reference kernel does (csrc/flash_attn_sm75.cu:548).
+    """
+    page_size = int(page_size)
+    sp, sp_t = validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
+                                        block_table)
+    _paged_kv_append_op(k_pages, v_pages, k_new, v_new, sp, sp_t, page_size, block_table)

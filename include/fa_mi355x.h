@@ -1,0 +1,134 @@
+/*
+ * fa_mi355x.h — C ABI of the MI355X (gfx950) attention path.
+ *
+ * This is the drop-in boundary that replaces the reference's torch extension
+ * `flashattention_custom._ext` (csrc/ext.cpp:91-116). Every entry point takes
+ * plain device pointers, sizes and an explicit HIP stream; nothing here
+ * allocates or frees device memory, and no torch type crosses the boundary.
+ *
+ * Conventions
+ *   - All tensors are dense, row-major ("contiguous") device buffers.
+ *   - fp16 buffers hold IEEE binary16 values; int32 buffers hold int32_t.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Work is
+ *     enqueued asynchronously; no entry point synchronises the host.
+ *   - The current HIP device must be the device that owns the buffers.
+ *   - Return value: 0 on success, a negative FA_ERR_* code otherwise; the
+ *     message of the last failure on the calling thread is fa_last_error().
+ *
+ * Paged K/V layout (reference: csrc/flash_attn_sm75.cu:54-86, ops.py:37-48)
+ *   k_pages, v_pages : fp16 [NB, Hk, P, PS, D]
+ *   Token `pos` of sequence b lives in logical page pos / PS, slot pos % PS.
+ *   Logical page p of sequence b maps to a physical page id phi:
+ *     block_table == NULL : phi = b * P + p               (reference identity map)
+ *     block_table != NULL : phi = block_table[b * max_blocks + p]
+ *   and phi addresses k_pages[phi / P, hk, phi % P, :, :]. Physical ids outside
+ *   [0, NB * P) and logical pages beyond the capacity (P, or max_blocks with a
+ *   block table) are never dereferenced: they read as absent keys and are
+ *   skipped on append.
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+/* element type of q / k / v / o */
+#define FA_DTYPE_F16 0
+#define FA_DTYPE_F32 1
+
+/* status codes */
+#define FA_OK 0
+#define FA_ERR_INVALID -1   /* an argument failed validation            */
+#define FA_ERR_LAUNCH  -2   /* the HIP runtime rejected a kernel launch */
+#define FA_ERR_WORKSPACE -3 /* workspace missing or smaller than needed */
+
+/*
+ * Contiguous attention: O = softmax(Q K^T / sqrt(D) + causal mask) V.
+ * Replaces _ext.flash_attn_fwd (csrc/ext.cpp:30-40) and its launcher
+ * flash_attn_fwd_cuda (csrc/flash_attn_sm75.cu:428-467).
+ *
+ *   q, o : [B, Hq, M, D]     k, v : [B, Hk, N, D]     dtype: FA_DTYPE_F16 | FA_DTYPE_F32
+ *   Hq % Hk == 0; q head h reads K/V head h / (Hq / Hk) (Hq == Hk is the
+ *   reference's MHA case). D in {64, 128}.
+ *   Key j is visible to query row i iff j < N and, when causal != 0,
+ *   k_off + j <= q_off + i, where q_off = q_offsets ? q_offsets[b] : q_offset
+ *   (likewise k_off). q_offsets / k_offsets are nullable int32 [B] buffers.
+ *   A row with no visible key (N > 0) yields NaN, and N == 0 yields zeros, as
+ *   in the reference's CPU math (flashattention_custom/ops.py:22-34).
+ */
+int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                      int dtype, int B, int Hq, int Hk, int M, int N, int D,
+                      int causal, int64_t q_offset, int64_t k_offset,
+                      const int32_t* q_offsets, const int32_t* k_offsets,
+                      void* stream);
+
+/*
+ * Paged attention over a K/V page pool (prefill chunk or single-token decode).
+ * Replaces _ext.flash_attn_paged_fwd (csrc/ext.cpp:42-68) and its launcher
+ * flash_attn_paged_fwd_cuda (csrc/flash_attn_sm75.cu:469-525).
+ *
+ *   q, o : fp16 [B, Hq, M, D]       k_pages, v_pages : fp16 [NB, Hk, P, PS, D]
+ *   seqlen   : int32 [B]   number of cached tokens of sequence b (clamped to
+ *                          the capacity P*PS, or max_blocks*PS)
+ *   head_map : int32 [Hq]  K/V head read by each query head (reference
+ *                          engine/llama_tp.py:145-156); an entry outside
+ *                          [0, Hk) makes that head's output NaN.
+ *   block_table : nullable int32 [B, max_blocks] (see header comment);
+ *                 without it NB must equal B.
+ *   Visibility and offsets as in fa_flash_attn_fwd with N = seqlen[b].
+ *   workspace : device scratch of at least fa_paged_workspace_bytes(...)
+ *               bytes for the same arguments (may be NULL when that is 0);
+ *               its contents need no initialisation.
+ */
+int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
+                            const int32_t* seqlen, int page_size,
+                            const int32_t* head_map, void* o,
+                            int B, int Hq, int M, int D, int NB, int Hk, int P,
+                            int causal, int64_t q_offset, int64_t k_offset,
+                            const int32_t* q_offsets, const int32_t* k_offsets,
+                            const int32_t* block_table, int max_blocks,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
+ * Workspace bytes fa_flash_attn_paged_fwd needs for these shapes. It depends
+ * only on host-known sizes (the per-sequence capacity in pages is P, or
+ * max_blocks when a block table is used), never on device contents.
+ */
+size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk,
+                                int capacity_pages, int page_size);
+
+/*
+ * Write T new tokens per sequence into their pages, in place:
+ *   k_pages[page(pos), hk, slot(pos), :] = k_new[b, hk, t, :]  (same for V),
+ *   pos = start + t, start = start_positions ? start_positions[b] : start_pos.
+ * Replaces _ext.paged_kv_append (csrc/ext.cpp:70-89) and paged_kv_append_cuda
+ * with its kernel (csrc/flash_attn_sm75.cu:528-588).
+ *   k_new, v_new : fp16 [B, Hk, T, D]    pages as above, D % 8 == 0.
+ * Positions whose page is negative or beyond the capacity, or whose physical
+ * page id is out of range, are skipped (reference kernel: :548).
+ */
+int fa_paged_kv_append(void* k_pages, void* v_pages,
+                       const void* k_new, const void* v_new,
+                       int B, int Hk, int T, int D, int NB, int P, int page_size,
+                       int64_t start_pos, const int32_t* start_positions,
+                       const int32_t* block_table, int max_blocks,
+                       void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fa_last_error(void);
+
+/* FA_ABI_VERSION of the loaded library. */
+int fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

@@ -1,0 +1,233 @@
+"""CPU tests of the drop-in boundary (no GPU needed).
+
+* libfa_mi355x.so loads and exports every function include/fa_mi355x.h declares.
+* The C ABI rejects bad arguments with status codes and the reference's
+  messages before touching the device.
+* The Python API keeps the reference's names, positional order and defaults
+  (flashattention_custom/ops.py:82-102) and raises the reference extension's
+  messages (csrc/ext.cpp:31-87) for bad arguments.
+* The custom ops are registered with shape-only (fake) implementations.
+"""
+import ctypes
+import inspect
+import os
+import re
+
+import pytest
+import torch
+
+from hrm_flashrenderer_amd import _lib, ops
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa_mi355x.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted([
+        "fa_abi_version", "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd", "fa_last_error",
+        "fa_paged_kv_append", "fa_paged_workspace_bytes"])
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert {s[0] for s in _lib.SYMBOLS} == set(declared_functions())
+    assert lib.fa_abi_version() == _lib.FA_ABI_VERSION
+
+
+def _status_and_message(rc):
+    return rc, _lib.load().fa_last_error().decode()
+
+
+def test_c_abi_rejects_bad_arguments_without_a_device():
+    lib = _lib.load()
+    P = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc, msg = _status_and_message(lib.fa_flash_attn_fwd(
+        P, P, P, P, 0, 1, 8, 8, 16, 16, 96, 1, 0, 0, None, None, None))
+    assert rc == -1 and msg == "Supported head_dim: 64 or 128"
+    rc, msg = _status_and_message(lib.fa_flash_attn_fwd(
+        P, P, P, P, 0, 1, 6, 4, 16, 16, 64, 1, 0, 0, None, None, None))
+    assert rc == -1 and msg == "H mismatch"
+    rc, msg = _status_and_message(lib.fa_flash_attn_fwd(
+        P, P, P, P, 7, 1, 8, 8, 16, 16, 64, 1, 0, 0, None, None, None))
+    assert rc == -1 and msg == "fp16 or fp32 required"
+    # paged: pool batch must equal B without a block table; page_size positive
+    rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 3, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+    assert rc == -1 and msg == "B mismatch"
+    rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
+        P, P, P, P, 0, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+    assert rc == -1 and msg == "page_size mismatch"
+    # decode path without its workspace
+    rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+    assert rc == -3 and msg.startswith("workspace of")
+    rc, msg = _status_and_message(lib.fa_paged_kv_append(
+        P, P, P, P, 2, 4, 3, 12, 2, 4, 16, 0, None, None, 0, None))
+    assert rc == -1 and msg == "head_dim must be a multiple of 8"
+    # empty work returns OK without any launch
+    assert lib.fa_flash_attn_fwd(P, P, P, P, 0, 0, 8, 8, 16, 16, 64, 1, 0, 0, None, None, None) == 0
+    assert lib.fa_paged_kv_append(P, P, P, P, 2, 4, 0, 128, 2, 4, 16, 0, None, None, 0, None) == 0
+
+
+def test_workspace_sizing_depends_on_sizes_only():
+    lib = _lib.load()
+    # decode (M = 1): (D + 2) floats per (b, hq, split), 256-byte aligned o part
+    ws = lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16)
+    nsplit = -(-1025 * 16 // 1024)
+    o_bytes = -(-(64 * 64 * nsplit * 128 * 4) // 256) * 256
+    assert ws == o_bytes + 64 * 64 * nsplit * 2 * 4
+    # prefill-shaped calls need no workspace
+    assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16) == 0
+    assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16) == 0
+
+
+def test_signatures_match_reference():
+    # flashattention_custom/ops.py:82, 88-89, 98
+    def params(fn):
+        return [(p.name, p.default) for p in inspect.signature(fn).parameters.values()
+                if p.kind is not inspect.Parameter.KEYWORD_ONLY]
+    E = inspect.Parameter.empty
+    assert params(ops.flash_attn) == [("q", E), ("k", E), ("v", E), ("causal", True),
+                                      ("q_offset", 0), ("k_offset", 0)]
+    assert params(ops.flash_attn_paged) == [
+        ("q", E), ("k_pages", E), ("v_pages", E), ("seqlen", E), ("page_size", E),
+        ("head_map", E), ("causal", True), ("q_offset", 0), ("k_offset", 0)]
+    assert params(ops.paged_kv_append) == [("k_pages", E), ("v_pages", E), ("k_new", E),
+                                           ("v_new", E), ("start_pos", E), ("page_size", E)]
+    import flashattention_custom
+    import flashattention_custom.ops as alias
+    assert alias.flash_attn_paged is ops.flash_attn_paged
+    assert flashattention_custom.__all__ == ["flash_attn", "flash_attn_paged", "paged_kv_append"]
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    q = torch.zeros(1, 8, 4, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="q/k/v must be CUDA"):
+        ops.flash_attn(q, q, q)
+    kp = torch.zeros(1, 8, 1, 16, 64, dtype=torch.float16)
+    sl = torch.zeros(1, dtype=torch.int32)
+    hm = torch.arange(8, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        ops.flash_attn_paged(q, kp, kp, sl, 16, hm)
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        ops.paged_kv_append(kp, kp, q[:, :, :1], q[:, :, :1], 0, 16)
+
+
+def _f16(*s):
+    return torch.zeros(*s, dtype=torch.float16)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: a.update(k=a["k"].float()), "fp16 required"),
+    (lambda a: a.update(q=_f16(1, 8, 64, 4).transpose(2, 3)), "contiguous required"),
+    (lambda a: a.update(q=_f16(8, 4, 64)), "q/k/v must be 4D"),
+    (lambda a: a.update(k=_f16(2, 8, 6, 64), v=_f16(2, 8, 6, 64)), "B mismatch"),
+    (lambda a: a.update(k=_f16(1, 3, 6, 64), v=_f16(1, 3, 6, 64)), "H mismatch"),
+    (lambda a: a.update(v=_f16(1, 8, 7, 64)), "N mismatch"),
+    (lambda a: a.update(q=_f16(1, 8, 4, 32)), "D mismatch"),
+    (lambda a: a.update(q=_f16(1, 8, 4, 96), k=_f16(1, 8, 6, 96), v=_f16(1, 8, 6, 96)),
+     "Supported head_dim: 64 or 128"),
+])
+def test_flash_attn_validation_messages(mutate, msg):
+    a = dict(q=_f16(1, 8, 4, 64), k=_f16(1, 8, 6, 64), v=_f16(1, 8, 6, 64))
+    ops.validate_flash_attn(**a, require_device=False)
+    mutate(a)
+    with pytest.raises(RuntimeError, match=msg):
+        ops.validate_flash_attn(**a, require_device=False)
+
+
+def _paged_args():
+    return dict(q=_f16(2, 8, 1, 128), k_pages=_f16(2, 2, 4, 16, 128),
+                v_pages=_f16(2, 2, 4, 16, 128), seqlen=torch.zeros(2, dtype=torch.int32),
+                page_size=16, head_map=(torch.arange(8) // 4).to(torch.int32))
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: a.update(v_pages=a["v_pages"].float()), "fp16 required"),
+    (lambda a: a.update(seqlen=a["seqlen"].long()), "seqlen int32 required"),
+    (lambda a: a.update(head_map=a["head_map"].long()), "head_map int32 required"),
+    (lambda a: a.update(q=_f16(2, 8, 2, 128)[:, :, :1]), "contiguous required"),
+    (lambda a: a.update(q=_f16(2, 8, 128)), r"q \[B,Hq,M,D\]"),
+    (lambda a: a.update(k_pages=_f16(2, 2, 64, 128)), r"k_pages/v_pages \[B,Hk,P,PS,D\]"),
+    (lambda a: a.update(v_pages=_f16(2, 2, 5, 16, 128)), "k_pages/v_pages mismatch"),
+    (lambda a: a.update(q=_f16(3, 8, 1, 128)), "B mismatch"),
+    (lambda a: a.update(head_map=torch.zeros(7, dtype=torch.int32)), "Hq mismatch"),
+    (lambda a: a.update(page_size=32), "page_size mismatch"),
+    (lambda a: a.update(q=_f16(2, 8, 1, 64)), "D mismatch"),
+    (lambda a: a.update(seqlen=torch.zeros(1, dtype=torch.int32)), r"seqlen \[B\] required"),
+    (lambda a: a.update(block_table=torch.zeros(3, 4, dtype=torch.int32)),
+     r"block_table \[B, max_blocks\] required"),
+    (lambda a: a.update(block_table=torch.zeros(2, 4, dtype=torch.int64)),
+     "block_table int32 required"),
+])
+def test_flash_attn_paged_validation_messages(mutate, msg):
+    a = _paged_args()
+    ops.validate_flash_attn_paged(**a, require_device=False)
+    mutate(a)
+    with pytest.raises(RuntimeError, match=msg):
+        ops.validate_flash_attn_paged(**a, require_device=False)
+
+
+def test_block_table_allows_a_shared_pool():
+    a = _paged_args()
+    a.update(k_pages=_f16(1, 2, 9, 16, 128), v_pages=_f16(1, 2, 9, 16, 128),
+             block_table=torch.zeros(2, 5, dtype=torch.int32))
+    assert ops.validate_flash_attn_paged(**a, require_device=False) == 5
+
+
+def _append_args():
+    return dict(k_pages=_f16(2, 4, 8, 128, 128), v_pages=_f16(2, 4, 8, 128, 128),
+                k_new=_f16(2, 4, 96, 128), v_new=_f16(2, 4, 96, 128), start_pos=145,
+                page_size=128)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda a: a.update(k_new=a["k_new"].float()), "fp16 required"),
+    (lambda a: a.update(k_pages=_f16(2, 4, 8, 128, 128).transpose(0, 1)), "contiguous required"),
+    (lambda a: a.update(k_new=_f16(2, 4, 96 * 128)), "shape mismatch"),
+    (lambda a: a.update(v_pages=_f16(2, 4, 9, 128, 128)), "k_pages/v_pages mismatch"),
+    (lambda a: a.update(v_new=_f16(2, 4, 95, 128)), "k_new/v_new mismatch"),
+    (lambda a: a.update(k_new=_f16(3, 4, 96, 128), v_new=_f16(3, 4, 96, 128)), "B mismatch"),
+    (lambda a: a.update(k_new=_f16(2, 2, 96, 128), v_new=_f16(2, 2, 96, 128)), "Hk mismatch"),
+    (lambda a: a.update(page_size=64), "page_size mismatch"),
+    (lambda a: a.update(k_new=_f16(2, 4, 96, 64), v_new=_f16(2, 4, 96, 64)), "D mismatch"),
+    (lambda a: a.update(start_pos=8 * 128 - 95), "exceeds the page capacity"),
+    (lambda a: a.update(start_pos=-1), "exceeds the page capacity"),
+    (lambda a: a.update(start_pos=torch.zeros(3, dtype=torch.int32)), r"start_pos \[B\] required"),
+])
+def test_paged_kv_append_validation_messages(mutate, msg):
+    a = _append_args()
+    assert ops.validate_paged_kv_append(**a, require_device=False) == (145, None)
+    mutate(a)
+    with pytest.raises(RuntimeError, match=msg):
+        ops.validate_paged_kv_append(**a, require_device=False)
+
+
+def test_custom_ops_have_shape_functions():
+    q = torch.empty(2, 8, 3, 128, dtype=torch.float16, device="meta")
+    kp = torch.empty(2, 2, 4, 16, 128, dtype=torch.float16, device="meta")
+    sl = torch.empty(2, dtype=torch.int32, device="meta")
+    hm = torch.empty(8, dtype=torch.int32, device="meta")
+    o = torch.ops.hrm_fa.flash_attn_paged(q, kp, kp, sl, 16, hm, True, 0, 0, None, None, None)
+    assert o.shape == q.shape and o.dtype == q.dtype
+    o2 = torch.ops.hrm_fa.flash_attn(q, q, q, True, 0, 0, None, None)
+    assert o2.shape == q.shape
+    kn = torch.empty(2, 2, 1, 128, dtype=torch.float16, device="meta")
+    assert torch.ops.hrm_fa.paged_kv_append(kp, kp, kn, kn, 0, None, 16, None) is None
+
+
+def test_product_path_does_not_import_the_oracle():
+    pkg = os.path.join(REPO, "hrm_flashrenderer_amd")
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(root, f)).read()
+                assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", src, re.M), f

@@ -1,0 +1,304 @@
+"""GPU parity of flash_attn / flash_attn_paged against the fp64 oracle.
+
+Bar: |out - ref| <= 2e-3 + 1e-2*|ref| elementwise (the fp32-softmax tolerance),
+NaN exactly where the reference yields NaN. Covers the reference's own
+known-answer tests (flash_tests/test_kernel.py:28-66) at their shapes, all
+five benchmark configurations (full size: every output for the decode
+configs, sampled heads for the prefill configs), block tables over a
+permuted shared pool with NaN-poisoned dead slots, per-sequence offsets,
+GQA and arbitrary head maps, and the edge cases (no keys, fully masked rows,
+invalid head-map entries, seqlen beyond capacity).
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from hrm_flashrenderer_amd import flash_attn, flash_attn_paged, paged_kv_append, workloads
+from oracle import attention as ora
+from paged_ref import (assert_close, decode_reference, paged_reference, poison_dead_slots,
+                       seeded)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "ref_cpu_path.npz")
+
+
+def _identity_pages(k, PS):
+    B, H, N, D = k.shape
+    P = (N + PS - 1) // PS
+    pages = torch.zeros(B, H, P, PS, D, dtype=k.dtype, device=k.device)
+    pages.view(B, H, P * PS, D)[:, :, :N] = k
+    return pages
+
+
+# -------------------------------------------------- reference KAT shapes ----
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_reference_kernel_kat(gpu, D):
+    """flash_tests/test_kernel.py:33-64: B=1, H=8, M=128, N=256, PS=128; contiguous,
+    paged (identity pages), and paged with q_offset=128, M=64."""
+    torch.manual_seed(0)
+    B, H, M, N, PS = 1, 8, 128, 256, 128
+    q, k, v = seeded((B, H, M, D), 100 + D), seeded((B, H, N, D), 101 + D), seeded((B, H, N, D), 102 + D)
+    out = flash_attn(q, k, v, causal=True, q_offset=0, k_offset=0)
+    ref = ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True)
+    assert_close(out.cpu(), ref, "contiguous")
+    kp, vp = _identity_pages(k, PS), _identity_pages(v, PS)
+    seqlen = torch.tensor([N], dtype=torch.int32, device=gpu)
+    hm = torch.arange(H, dtype=torch.int32, device=gpu)
+    outp = flash_attn_paged(q, kp, vp, seqlen, PS, hm, causal=True, q_offset=0, k_offset=0)
+    assert_close(outp.cpu(), ref, "paged")
+    q2 = seeded((B, H, 64, D), 103 + D)
+    outp2 = flash_attn_paged(q2, kp, vp, seqlen, PS, hm, causal=True, q_offset=128, k_offset=0)
+    ref2 = ora.attention_f64(q2.cpu(), k.cpu(), v.cpu(), True, 128, 0)
+    assert_close(outp2.cpu(), ref2, "paged offset")
+
+
+def test_golden_reference_outputs(gpu):
+    """GPU results are within tolerance of the reference CPU path's own outputs
+    (tests/golden) and of the fp64 form on the same inputs."""
+    g = np.load(GOLDEN, allow_pickle=False)
+    for name in ("attn_f16_causal", "attn_f16_offset", "attn_f32_causal", "attn_f32_noncausal",
+                 "attn_f16_kofs"):
+        causal, qo, ko = g[f"{name}/meta"].tolist()
+        q, k, v = (torch.from_numpy(g[f"{name}/{x}"]).to(gpu) for x in "qkv")
+        out = flash_attn(q, k, v, bool(causal), qo, ko).cpu()
+        assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), bool(causal), qo, ko), name)
+        assert_close(out, g[f"{name}/o"], name + " vs reference output")
+    for name in ("paged_prefill", "paged_decode", "paged_decode_mha"):
+        causal, qo, ko, ps = g[f"{name}/meta"].tolist()
+        t = {x: torch.from_numpy(g[f"{name}/{x}"]).to(gpu)
+             for x in ("q", "k_pages", "v_pages", "seqlen", "head_map")}
+        out = flash_attn_paged(t["q"], t["k_pages"], t["v_pages"], t["seqlen"], ps, t["head_map"],
+                               bool(causal), qo, ko).cpu()
+        B = t["q"].size(0)
+        kk = ora.gather_kv(g[f"{name}/k_pages"], B, ps)
+        vv = ora.gather_kv(g[f"{name}/v_pages"], B, ps)
+        ref = ora.attention_f64(g[f"{name}/q"], kk, vv, bool(causal), qo, ko,
+                                kv_len=g[f"{name}/seqlen"], head_map=g[f"{name}/head_map"])
+        assert_close(out, ref, name)
+        assert_close(out, g[f"{name}/o"], name + " vs reference output")
+
+
+# ------------------------------------------------------ contiguous path ----
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_cfg1_causal_mha(gpu, dtype):
+    q, k, v = workloads.cfg1(gpu, dtype)
+    out = flash_attn(q, k, v)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert_close(out.cpu(), ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True), f"cfg1 {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+def test_contiguous_gqa_offsets_noncausal(gpu, dtype, D):
+    B, Hq, Hk, M, N = 3, 6, 2, 77, 150
+    q, k, v = seeded((B, Hq, M, D), 1, dtype), seeded((B, Hk, N, D), 2, dtype), seeded((B, Hk, N, D), 3, dtype)
+    for causal, qo, ko in ((True, 0, 0), (True, 73, 0), (False, 0, 0), (True, 5, 9)):
+        out = flash_attn(q, k, v, causal, qo, ko).cpu()
+        assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal, qo, ko),
+                     f"{dtype} D={D} causal={causal} qo={qo} ko={ko}")
+    qo_t = torch.tensor([0, 40, 73], dtype=torch.int32, device=gpu)
+    out = flash_attn(q, k, v, True, qo_t, 0).cpu()
+    assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True, [0, 40, 73], 0),
+                 "per-sequence q_offset")
+
+
+# ----------------------------------------------------------- paged path ----
+
+def _small_paged(B, Hq, Hk, M, lengths, PS=16, D=128, seed=0, causal=True, q_offsets=None,
+                 spare_pages=5):
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(seed)
+    pages = [(n + PS - 1) // PS for n in lengths]
+    total = sum(pages) + spare_pages
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    max_blocks = max(pages) + 2
+    bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[pos:pos + n]
+        pos += n
+    kp = seeded((1, Hk, total, PS, D), seed + 1)
+    vp = seeded((1, Hk, total, PS, D), seed + 2)
+    q = seeded((B, Hq, M, D), seed + 3)
+    poison_dead_slots(kp, vp, bt, lengths, PS)
+    return dict(q=q, kp=kp, vp=vp, bt=bt.to(dev), lengths=lengths,
+                seqlen=torch.tensor(lengths, dtype=torch.int32, device=dev),
+                hm=(torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(dev), PS=PS,
+                causal=causal, q_offsets=q_offsets)
+
+
+def _run_and_check(c, what, rows=None):
+    qo = c["q_offsets"]
+    qo_arg = 0 if qo is None else torch.tensor(qo, dtype=torch.int32, device=c["q"].device)
+    out = flash_attn_paged(c["q"], c["kp"], c["vp"], c["seqlen"], c["PS"], c["hm"], c["causal"],
+                           qo_arg, 0, block_table=c["bt"]).cpu().numpy()
+    ref = paged_reference(c["q"], c["kp"], c["vp"], c["bt"], c["lengths"], c["PS"], c["hm"],
+                          c["causal"], qo)
+    for (b, h), r in ref.items():
+        assert_close(out[b, h], r, f"{what} b={b} h={h}")
+    return out
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_prefill_gqa_block_table(gpu, D):
+    c = _small_paged(2, 10, 2, 300, [300, 300], D=D, seed=10 + D)
+    _run_and_check(c, "prefill")
+
+
+def test_chunked_prefill_per_sequence_offsets(gpu):
+    prior = [0, 37, 150, 600]
+    M = 130
+    lengths = [p + M for p in prior]
+    c = _small_paged(4, 8, 1, M, lengths, seed=20, q_offsets=prior)
+    _run_and_check(c, "chunked prefill")
+
+
+@pytest.mark.parametrize("Hq,Hk,lengths", [(40, 8, [512, 1000, 17, 2047]),
+                                           (64, 8, [1025, 16, 3000]),
+                                           (8, 8, [5, 700]), (32, 1, [300, 1])])
+def test_decode_m1(gpu, Hq, Hk, lengths):
+    c = _small_paged(len(lengths), Hq, Hk, 1, lengths, seed=30, causal=False)
+    _run_and_check(c, f"decode {Hq}/{Hk}")
+
+
+@pytest.mark.parametrize("M,causal", [(2, True), (3, False), (4, True), (16, True)])
+def test_decode_few_rows(gpu, M, causal):
+    lengths = [400, 1500, 33]
+    c = _small_paged(3, 40, 8, M, lengths, seed=40 + M, causal=causal,
+                     q_offsets=[n - M for n in lengths] if causal else None)
+    _run_and_check(c, f"M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 200])
+def test_arbitrary_head_map(gpu, M):
+    c = _small_paged(2, 6, 3, M, [700, 260], seed=50, causal=M > 1)
+    c["hm"] = torch.tensor([2, 0, 2, 1, 2, 0], dtype=torch.int32, device=gpu)
+    _run_and_check(c, "head_map")
+
+
+@pytest.mark.parametrize("PS", [128, 24, 8])
+def test_page_sizes_identity_layout(gpu, PS):
+    """Reference layout [B, Hk, P, PS, D] without a block table."""
+    B, Hq, Hk, D = 2, 4, 2, 128
+    lengths = [3 * PS + 5, PS - 1]
+    P = 4
+    kp, vp = seeded((B, Hk, P, PS, D), 60), seeded((B, Hk, P, PS, D), 61)
+    bt_id = torch.arange(B * P, dtype=torch.int32).view(B, P)   # identity map phi = b*P + p
+    poison_dead_slots(kp, vp, bt_id, lengths, PS)
+    seqlen = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    hm = (torch.arange(Hq) // 2).to(torch.int32).to(gpu)
+    for M, causal in ((1, False), (70, True)):
+        q = seeded((B, Hq, M, D), 62 + M)
+        qo = torch.tensor([n - M for n in lengths], dtype=torch.int32, device=gpu)
+        out = flash_attn_paged(q, kp, vp, seqlen, PS, hm, causal, qo if causal else 0).cpu()
+        for b in range(B):
+            n = lengths[b]
+            kk = kp[b].reshape(Hk, P * PS, D)[:, :n].cpu()[None]
+            vv = vp[b].reshape(Hk, P * PS, D)[:, :n].cpu()[None]
+            ref = ora.attention_f64(q[b:b + 1].cpu(), kk, vv, causal,
+                                    int(qo[b]) if causal else 0, 0)
+            assert_close(out[b:b + 1], ref, f"PS={PS} M={M} b={b}")
+
+
+def test_edge_cases(gpu):
+    B, Hq, Hk, PS, D = 3, 4, 2, 16, 128
+    kp, vp = seeded((B, Hk, 4, PS, D), 70), seeded((B, Hk, 4, PS, D), 71)
+    hm = torch.tensor([0, 1, 5, -1], dtype=torch.int32, device=gpu)   # heads 2, 3 invalid
+    seqlen = torch.tensor([0, 40, 1000], dtype=torch.int32, device=gpu)  # 1000 > capacity 64
+    for M, causal, ko in ((1, False, 0), (40, True, 0), (1, True, 50), (40, True, 50)):
+        q = seeded((B, Hq, M, D), 72 + M)
+        out = flash_attn_paged(q, kp, vp, seqlen, PS, hm, causal, 0, ko).cpu()
+        assert torch.isnan(out[:, 2:]).all()
+        assert (out[0, :2] == 0).all()                 # no keys -> zeros (ops.py semantics)
+        for b in (1, 2):
+            n = min(int(seqlen[b]), 64)
+            kk = kp[b].reshape(Hk, 64, D)[:, :n].cpu()[None]
+            vv = vp[b].reshape(Hk, 64, D)[:, :n].cpu()[None]
+            ref = ora.attention_f64(q[b:b + 1, :2].cpu(), kk, vv, causal, 0, ko,
+                                    head_map=[0, 1])
+            assert_close(out[b:b + 1, :2], ref, f"edge M={M} causal={causal} ko={ko} b={b}")
+
+
+def test_deterministic(gpu):
+    c = _small_paged(2, 40, 8, 1, [5000, 3333], seed=80, causal=False)
+    a = flash_attn_paged(c["q"], c["kp"], c["vp"], c["seqlen"], 16, c["hm"], False,
+                         block_table=c["bt"])
+    b = flash_attn_paged(c["q"], c["kp"], c["vp"], c["seqlen"], 16, c["hm"], False,
+                         block_table=c["bt"])
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------ full-size configurations ----
+
+@pytest.mark.parametrize("cfg", ["cfg3", "cfg4"])
+def test_full_size_decode(gpu, cfg):
+    w = getattr(workloads, cfg)(gpu)
+    if w.k_new is not None:
+        paged_kv_append(w.k_pool, w.v_pool, w.k_new, w.v_new, w.append_pos, 16,
+                        block_table=w.block_table)
+    poison_dead_slots(w.k_pool, w.v_pool, w.block_table, w.lengths, 16)
+    out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, False,
+                           block_table=w.block_table).cpu().numpy()
+    ref = decode_reference(w)
+    assert_close(out, ref, cfg)
+
+
+def test_full_size_prefill_cfg2_sampled_heads(gpu):
+    w = workloads.cfg2(gpu)
+    out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True,
+                           block_table=w.block_table).cpu().numpy()
+    assert np.isfinite(out).all()
+    pairs = [(0, 0), (1, 17), (2, 26), (3, 39)]
+    ref = paged_reference(w.q, w.k_pool, w.v_pool, w.block_table, w.lengths, 16, w.head_map,
+                          True, None, pairs=pairs)
+    for (b, h), r in ref.items():
+        assert_close(out[b, h], r, f"cfg2 b={b} h={h}")
+
+
+def test_full_size_chunked_prefill_cfg5_sampled_heads(gpu):
+    w = workloads.cfg5(gpu)
+    poison_dead_slots(w.k_pool, w.v_pool, w.block_table, w.lengths, 16)
+    out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True,
+                           w.q_offsets, block_table=w.block_table).cpu().numpy()
+    assert np.isfinite(out).all()
+    pairs = [(b, (7 * b) % 64) for b in range(0, 16, 3)]
+    ref = paged_reference(w.q, w.k_pool, w.v_pool, w.block_table, w.lengths, 16, w.head_map,
+                          True, w.q_offsets_host, pairs=pairs)
+    for (b, h), r in ref.items():
+        assert_close(out[b, h], r, f"cfg5 b={b} h={h}")
+
+
+# -------------------------------------------------- reference call pattern ----
+
+def test_llama_tp_call_pattern_through_alias_package(gpu):
+    """engine/llama_tp.py:59-78 and :171-200: append the chunk's K/V with one
+    scalar start, set seqlen, then attend with causal=prefill and
+    q_offset=start, through `flashattention_custom.ops` (the reference name)."""
+    from flashattention_custom.ops import flash_attn_paged as fap, paged_kv_append as pka
+    B, Hq, Hk, D, PS, P = 2, 8, 2, 128, 128, 4
+    k_pages = torch.empty(B, Hk, P, PS, D, dtype=torch.float16, device=gpu)
+    v_pages = torch.empty_like(k_pages)
+    seqlen = torch.zeros(B, dtype=torch.int32, device=gpu)
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    ks, vs, outs, qs = [], [], [], []
+    cur = 0
+    for step, T in enumerate([200, 1, 1, 57]):
+        q = seeded((B, Hq, T, D), 90 + step)
+        k = seeded((B, Hk, T, D), 190 + step)
+        v = seeded((B, Hk, T, D), 290 + step)
+        pka(k_pages, v_pages, k, v, start_pos=cur, page_size=PS)
+        cur += T
+        seqlen.fill_(cur)
+        out = fap(q=q, k_pages=k_pages, v_pages=v_pages, seqlen=seqlen, page_size=PS,
+                  head_map=hm, causal=bool(T > 1), q_offset=cur - T, k_offset=0)
+        ks.append(k), vs.append(v), outs.append(out), qs.append(q)
+        kall = torch.cat(ks, dim=2).cpu()
+        vall = torch.cat(vs, dim=2).cpu()
+        ref = ora.attention_f64(q.cpu(), kall, vall, T > 1, cur - T, 0)
+        assert_close(out.cpu(), ref, f"step {step}")
