@@ -69,16 +69,29 @@ struct DecodeRegs {
 
 // Loads the K/V fragments of one 16-token group (rows beyond `t_end` or not
 // addressable read as zero, so masked keys never carry NaN garbage into P V).
-template <int D>
+// ALIGNED (pages of a multiple of 16 tokens, or contiguous K/V): the group sits
+// in one page, found by one wave-uniform (scalar) block-table read, so no
+// vector-memory wait separates the group's loads from the ones in flight.
+template <int D, bool ALIGNED>
 __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p, const f16* kp,
                                            const f16* vp, int b, int hk, int t0, int t_end,
                                            int n, int quarter) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
   constexpr int VW = DecodeRegs<D>::VW;
+  int64_t gbase = -1;
+  if constexpr (ALIGNED) gbase = p.kv.row_offset(b, hk, t0);  // t0 < t_end <= capacity
+  auto row_off = [&](int row) -> int64_t {
+    if (row >= t_end) return -1;
+    if constexpr (ALIGNED) {
+      return gbase < 0 ? -1 : gbase + (int64_t)(row - t0) * D;
+    } else {
+      return p.kv.row_offset(b, hk, row);
+    }
+  };
   {
     const int row = t0 + n;
-    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
+    const int64_t off = row_off(row);
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
       if (off >= 0) {
@@ -91,7 +104,7 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + 4 * quarter + i;
-    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
+    const int64_t off = row_off(row);
     if constexpr (VW == 4) {
       u32x4 x = u32x4{0u, 0u, 0u, 0u};
       if (off >= 0) x = *reinterpret_cast<const u32x4*>(vp + off + DPL * n);
@@ -106,7 +119,7 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
   }
 }
 
-template <int D>
+template <int D, bool ALIGNED>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
@@ -197,12 +210,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams
 
     int g = g_begin + wave;
     DecodeRegs<D> cur;
-    if (g < g_end) load_group<D>(cur, p, kp, vp, b, hk, g << 4, t_end, n, quarter);
+    if (g < g_end) load_group<D, ALIGNED>(cur, p, kp, vp, b, hk, g << 4, t_end, n, quarter);
     while (g < g_end) {
       const int t0 = g << 4;
       const int g_next = g + kDecodeWaves;
       DecodeRegs<D> nxt;
-      if (g_next < g_end) load_group<D>(nxt, p, kp, vp, b, hk, g_next << 4, t_end, n, quarter);
+      if (g_next < g_end)
+        load_group<D, ALIGNED>(nxt, p, kp, vp, b, hk, g_next << 4, t_end, n, quarter);
 
       // S^T[token][row] for the 16 tokens of the group.
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -394,13 +408,21 @@ hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
   const dim3 grid((unsigned)p.nsplit, (unsigned)p.Hk, (unsigned)p.B);
   const int rows = p.B * p.Hq * p.M;
   const dim3 cgrid((unsigned)((rows + 3) / 4));
+  const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
+  const dim3 block(kDecodeThreads);
   if (D == 128) {
-    hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(kDecodeThreads), 0, stream, p);
+    if (aligned)
+      hipLaunchKernelGGL((decode_split_kernel<128, true>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_split_kernel<128, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
   } else {
-    hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(kDecodeThreads), 0, stream, p);
+    if (aligned)
+      hipLaunchKernelGGL((decode_split_kernel<64, true>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_split_kernel<64, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(256), 0, stream, p);

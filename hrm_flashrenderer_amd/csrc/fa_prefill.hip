@@ -58,33 +58,58 @@ struct TileRegs {
   u32x4 v[KPT];
 };
 
-template <int D>
+__device__ __forceinline__ int64_t pick4(const int64_t (&v)[4], int g) {
+  return g == 0 ? v[0] : g == 1 ? v[1] : g == 2 ? v[2] : v[3];
+}
+
+// Fetches the K/V rows of the 64-key tile starting at k0 into registers.
+// Rows at or beyond kv_len (or not addressable) read as zero.
+//
+// ALIGNED (contiguous K/V, or pages of a multiple of 16 tokens): the 16 keys
+// of each quarter of the tile share one page, so the page lookup is one
+// uniform (scalar) block-table read per quarter and rows are plain offsets
+// from it. Scalar reads complete on their own counter, so the vector loads of
+// the tile are issued back to back and stay in flight while the current tile
+// is computed. Otherwise every row is looked up on its own.
+template <int D, bool ALIGNED>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, const AttnParams& p, const f16* kp,
                                           const f16* vp, int b, int hk, int k0, int kv_len,
                                           int tid) {
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int KCH = TileRegs<D>::KCH;
   constexpr int KPT = TileRegs<D>::KPT;
+  constexpr int RPP = kThreads / CPR;  // rows per pass of the K loader
+  int64_t goff[4];
+  if constexpr (ALIGNED) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int key = k0 + 16 * g;
+      goff[g] = key < kv_len ? p.kv.row_offset(b, hk, key) : -1;
+    }
+  }
+  auto row_off = [&](int row) -> int64_t {
+    const int j = k0 + row;
+    if (j >= kv_len) return -1;
+    if constexpr (ALIGNED) {
+      const int64_t base = pick4(goff, row >> 4);
+      return base < 0 ? -1 : base + (int64_t)(row & 15) * D;
+    } else {
+      return p.kv.row_offset(b, hk, j);
+    }
+  };
+  const int col = tid % CPR;
 #pragma unroll
   for (int i = 0; i < KCH; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / CPR;
-    const int col = c % CPR;
-    const int j = k0 + row;
-    const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
+    const int64_t off = row_off(tid / CPR + RPP * i);
     r.k[i] = off >= 0 ? *reinterpret_cast<const u32x4*>(kp + off + 8 * col)
                       : u32x4{0u, 0u, 0u, 0u};
   }
-  {
-    const int kg = tid / CPR;  // key group: keys KPT*kg .. +KPT
-    const int dc = tid % CPR;  // d chunk: d = 8*dc .. +8
+  const int kg = tid / CPR;  // key group: keys KPT*kg .. +KPT
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int j = k0 + KPT * kg + i;
-      const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
-      r.v[i] = off >= 0 ? *reinterpret_cast<const u32x4*>(vp + off + 8 * dc)
-                        : u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < KPT; ++i) {
+    const int64_t off = row_off(KPT * kg + i);
+    r.v[i] = off >= 0 ? *reinterpret_cast<const u32x4*>(vp + off + 8 * col)
+                      : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -121,7 +146,7 @@ __device__ __forceinline__ void store_tile(const TileRegs<D>& r, f16* sK, f16* s
   }
 }
 
-template <int D>
+template <int D, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   constexpr int KSTEPS = D / 16;  // k-steps of S^T
   constexpr int DBLK = D / 32;    // 32-row blocks of O^T
@@ -186,14 +211,14 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   const float c = p.scale_log2;
 
   TileRegs<D> regs;
-  if (ntiles > 0) load_tile<D>(regs, p, kp, vp, b, hk, 0, kv_len, tid);
+  if (ntiles > 0) load_tile<D, ALIGNED>(regs, p, kp, vp, b, hk, 0, kv_len, tid);
 
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = t * kBN;
     __syncthreads();
     store_tile<D>(regs, sK, sVt, tid);
     __syncthreads();
-    if (t + 1 < ntiles) load_tile<D>(regs, p, kp, vp, b, hk, k0 + kBN, kv_len, tid);
+    if (t + 1 < ntiles) load_tile<D, ALIGNED>(regs, p, kp, vp, b, hk, k0 + kBN, kv_len, tid);
     if (k0 >= wave_lim_max) continue;
 
     // S^T[key][row]: two 32-key blocks.
@@ -374,10 +399,18 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
     return hipGetLastError();
   }
   const dim3 grid((unsigned)((p.M + kBM - 1) / kBM), (unsigned)p.Hq, (unsigned)p.B);
-  if (D == 128)
-    hipLaunchKernelGGL(prefill_f16_kernel<128>, grid, dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL(prefill_f16_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+  const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
+  if (D == 128) {
+    if (aligned)
+      hipLaunchKernelGGL((prefill_f16_kernel<128, true>), grid, dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_f16_kernel<128, false>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    if (aligned)
+      hipLaunchKernelGGL((prefill_f16_kernel<64, true>), grid, dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_f16_kernel<64, false>), grid, dim3(kThreads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -209,7 +209,7 @@ def roofline_peaks():
 
 
 def sample_meta(w: PagedWorkload) -> dict:
-    return dict(B=w.B, Hq=w.Hq, Hk=w.Hk, M=w.M, D=w.D, page_size=PAGE,
+    return dict(B=w.B, Hq=w.Hq, Hk=w.Hk, M=w.M, D=w.D,
                 kv_tokens=int(sum(w.lengths)), min_len=int(min(w.lengths)),
                 max_len=int(max(w.lengths)), **w.meta)
 
