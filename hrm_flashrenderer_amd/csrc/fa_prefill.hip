@@ -301,6 +301,264 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tile-DMA prefill (pages of a multiple of 16 tokens, or contiguous K/V).
+//
+//  * K and V tiles of 64 keys go from HBM straight into LDS with
+//    buffer_load ... lds (16 bytes per lane), no staging registers. Each wave
+//    moves one 16-key quarter of the tile, which lies in one page, through one
+//    buffer resource whose size covers only the quarter's valid rows: rows
+//    past seqlen land in LDS as zeros.
+//  * LDS holds two K and two V tiles (double buffer, one barrier per tile).
+//    Rows are 2*D bytes; 16-byte chunks are XOR-swizzled per row so that the
+//    reads below are free of bank conflicts: K chunk c of row r is stored at
+//    c ^ (r % CH) (32 rows read at one column by ds_read_b128), V chunk c at
+//    c ^ (4r % CH) (4 rows x 32 bytes per 16 lanes for the transposing read).
+//  * S^T = K Q^T (A = K from LDS, B = Q in registers) and O^T = V^T P^T with
+//    v_mfma_f32_32x32x16_f16. The V^T operand comes from ds_read_b64_tr_b16:
+//    in each 16-lane group, lane s points at V[k0 + s/4][d0 + 4(s%4)] and
+//    lane i receives V[k0 + j][d0 + i], j = 0..3 (4 keys of one d).
+//  * Online softmax keeps a per-row reference max and rescales O only when a
+//    tile's max exceeds it by more than 2^8 (then P <= 256 fits fp16 exactly as
+//    well as P <= 1 does; the final division uses the same reference).
+//  * Work order is XCD-aware: consecutive dispatch slots go round-robin over
+//    the 8 XCDs, so slot L runs item (L % 8) * per_xcd + L / 8 of a list
+//    ordered by (sequence, KV-head group, q tile descending, head in group):
+//    all q tiles and heads that share one KV head run on one XCD's L2, longest
+//    rows first.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
+constexpr float kRescaleLog2 = 8.f;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           (int)kRsrcWord3);
+}
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+template <int D>
+struct DmaCfg {
+  static constexpr int ROWB = 2 * D;             // bytes per key row
+  static constexpr int CH = D / 8;               // 16-byte chunks per row
+  static constexpr int TILE = kBN * ROWB;        // bytes per K (or V) tile
+  static constexpr int RPI = 1024 / ROWB;        // rows per wave-wide 16-byte load
+  static constexpr int IPQ = 16 / RPI;           // loads per 16-key quarter
+  __device__ static int swz_k(int row) { return row % CH; }
+  __device__ static int swz_v(int row) { return (4 * row) % CH; }
+};
+
+// Issue the DMA of one 64-key tile (wave w moves keys k0+16w .. +15).
+template <int D>
+__device__ __forceinline__ void dma_tile(const AttnParams& p, const char* kp, const char* vp,
+                                         int b, int hk, int k0, int kv_len, int wave, int lane,
+                                         char* sK, char* sV) {
+  using C = DmaCfg<D>;
+  const int g0 = k0 + 16 * wave;
+  const int valid = min(16, kv_len - g0);
+  int64_t off = 0;
+  uint32_t nbytes = 0;
+  if (valid > 0) {
+    off = p.kv.row_offset(b, hk, g0);
+    nbytes = off >= 0 ? (uint32_t)(valid * C::ROWB) : 0u;
+    off = off >= 0 ? off : 0;
+  }
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + off * 2, nbytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + off * 2, nbytes);
+  const int pch = lane % C::CH;
+#pragma unroll
+  for (int i = 0; i < C::IPQ; ++i) {
+    const int rq = C::RPI * i + lane / C::CH;  // row within the quarter
+    const int rt = 16 * wave + rq;             // row within the tile
+    const uint32_t vk = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_k(rt)));
+    const uint32_t vv = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_v(rt)));
+    const int dst = (16 * wave + C::RPI * i) * C::ROWB;  // 1 KB block of rows rt - rq + RPI*i
+    lds_dma16(rk, sK + dst, vk);
+    lds_dma16(rv, sV + dst, vv);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, int ntq,
+                                                                  int group, int per_xcd,
+                                                                  int total) {
+  using C = DmaCfg<D>;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * C::TILE];  // K0 V0 K1 V1
+
+  // ---- work item (XCD-aware order) ----
+  const int slot = blockIdx.x;
+  const int item = (slot & 7) * per_xcd + (slot >> 3);
+  if (item >= total) return;
+  const int per_pair = ntq * group;
+  const int pair = item / per_pair;
+  const int rem = item - pair * per_pair;
+  const int qt = ntq - 1 - rem / group;
+  const int ngroups = p.Hq / group;
+  const int hq = (pair % ngroups) * group + rem % group;
+  const int b = pair / ngroups;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31;
+  const int half_id = lane >> 5;
+  const int q0 = qt * kBM;
+  const int qrow = q0 + wave * 32 + col;
+  f16* op = reinterpret_cast<f16*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
+
+  const int hk = p.kv_head(hq);
+  if (hk < 0) {
+    if (qrow < p.M) {
+      for (int d = half_id * (D / 2); d < (half_id + 1) * (D / 2); ++d)
+        op[(int64_t)qrow * D + d] = (f16)__builtin_nanf("");
+    }
+    return;
+  }
+
+  const int kv_len = p.kv_len(b);
+  const int qo = p.q_off(b);
+  const int ko = p.k_off(b);
+  const int last_row = min(q0 + kBM, p.M) - 1;
+  const int wg_lim = row_key_limit(kv_len, p.causal, qo, ko, last_row);
+  const int ntiles = (wg_lim + kBN - 1) / kBN;
+  const int wrow0 = q0 + wave * 32;
+  const int wrow1 = min(wrow0 + 31, p.M - 1);
+  const bool wave_rows = wrow0 < p.M;
+  const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
+  const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
+  const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
+
+  const char* kp = reinterpret_cast<const char*>(p.k);
+  const char* vp = reinterpret_cast<const char*>(p.v);
+  if (ntiles > 0) dma_tile<D>(p, kp, vp, b, hk, 0, kv_len, wave, lane, smem, smem + C::TILE);
+
+  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  half8 qreg[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    qreg[ks] = qrow < p.M
+                   ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
+                   : half8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  // Per-lane LDS byte offsets (buffer 0; buffer 1 is +2*TILE).
+  // K: row 32*mb + col, logical chunk 2*ks + half_id.
+  int koff[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks)
+    koff[ks] = col * C::ROWB + 16 * ((2 * ks + half_id) ^ C::swz_k(col));
+  // V (transposing read): 16-lane group gq, lane sl -> row 4*(gq/2) + sl/4 (+16s, +8),
+  // d = 32*i + 16*(gq%2) + 4*(sl%4).
+  const int gq = lane >> 4, sl = lane & 15;
+  const int vrow = 4 * (gq >> 1) + (sl >> 2);
+  int voff[DBLK];
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) {
+    const int d = 32 * i + 16 * (gq & 1) + 4 * (sl & 3);
+    voff[i] = C::TILE + vrow * C::ROWB + 16 * ((d >> 3) ^ C::swz_v(vrow)) + 2 * (d & 7);
+  }
+
+  floatx16 acc_o[DBLK];
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) acc_o[i] = floatx16{};
+  float m_ref = -INFINITY;  // scaled (log2) reference max
+  float l_run = 0.f;
+  const float c = p.scale_log2;
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = t * kBN;
+    char* buf = smem + (t & 1) * 2 * C::TILE;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 < ntiles) {
+      char* nbuf = smem + ((t + 1) & 1) * 2 * C::TILE;
+      dma_tile<D>(p, kp, vp, b, hk, k0 + kBN, kv_len, wave, lane, nbuf, nbuf + C::TILE);
+    }
+    if (k0 >= wave_lim_max) continue;
+
+    floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const half8 a0 = *reinterpret_cast<const half8*>(buf + koff[ks]);
+      const half8 a1 = *reinterpret_cast<const half8*>(buf + koff[ks] + 32 * C::ROWB);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
+    }
+    if (k0 + kBN > wave_lim_min) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * half_id + (r & 3);
+        if (key >= lim) s0[r] = -INFINITY;
+        if (key + 32 >= lim) s1[r] = -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+    if (__builtin_amdgcn_ballot_w64(mx > m_ref + kRescaleLog2) != 0) {
+      const float m_new = fmaxf(m_ref, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i) acc_o[i] = acc_o[i] * alpha;
+      m_ref = m_new;
+    }
+    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -m_use));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -m_use));
+      psum += s0[r] + s1[r];
+    }
+    l_run += psum;
+    half8 pb[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pb[0][j] = (f16)s0[j];
+      pb[1][j] = (f16)s0[8 + j];
+      pb[2][j] = (f16)s1[j];
+      pb[3][j] = (f16)s1[8 + j];
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i) {
+        const char* va = buf + voff[i] + 16 * s * C::ROWB;
+        const half4 lo = __builtin_bit_cast(
+            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (__attribute__((address_space(3))) short4v*)(va)));
+        const half4 hi = __builtin_bit_cast(
+            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (__attribute__((address_space(3))) short4v*)(va + 8 * C::ROWB)));
+        const half8 a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[s], acc_o[i], 0, 0, 0);
+      }
+    }
+  }
+
+  if (qrow >= p.M) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
+  f16* orow = op + (int64_t)qrow * D;
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
+                            (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      *reinterpret_cast<half4*>(orow + 32 * i + 8 * g + 4 * half_id) = h;
+    }
+  }
+}
+
 // fp32 contiguous attention (the reference's CPU path accepts fp32,
 // flashattention_custom/ops.py:22-34). Exact fp32 arithmetic on the vector
 // ALUs: one wave of 64 query rows per workgroup, Q rows in LDS, K/V streamed
@@ -398,8 +656,22 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
       hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(64), 0, stream, p);
     return hipGetLastError();
   }
-  const dim3 grid((unsigned)((p.M + kBM - 1) / kBM), (unsigned)p.Hq, (unsigned)p.B);
   const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
+  const int ntq = (p.M + kBM - 1) / kBM;
+  if (aligned) {
+    const int group = (p.Hk > 0 && p.Hq % p.Hk == 0) ? p.Hq / p.Hk : 1;
+    const int total = ntq * p.Hq * p.B;
+    const int per_xcd = (total + 7) / 8;
+    const dim3 g1((unsigned)(8 * per_xcd));
+    if (D == 128)
+      hipLaunchKernelGGL(prefill_dma_kernel<128>, g1, dim3(kThreads), 0, stream, p, ntq, group,
+                         per_xcd, total);
+    else
+      hipLaunchKernelGGL(prefill_dma_kernel<64>, g1, dim3(kThreads), 0, stream, p, ntq, group,
+                         per_xcd, total);
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)ntq, (unsigned)p.Hq, (unsigned)p.B);
   if (D == 128) {
     if (aligned)
       hipLaunchKernelGGL((prefill_f16_kernel<128, true>), grid, dim3(kThreads), 0, stream, p);
