@@ -17,6 +17,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -42,27 +43,37 @@ struct KVMap {
   int paged;                   // 0: contiguous K/V
 
   // Element offset of row j of (b, hk); -1 when the row is not addressable
-  // (page beyond the capacity or an out-of-range physical id).
+  // (page beyond the capacity or an out-of-range physical id). With uniform
+  // arguments every step is scalar: the block table is read through the
+  // constant address space (s_load), and the physical id is split into
+  // (pool row, page) only when the pool has more than one row.
   __device__ __forceinline__ int64_t row_offset(int b, int hk, int j) const {
     if (!paged) return (int64_t)b * stride_nb + (int64_t)hk * stride_hk + (int64_t)j * D;
-    int page, slot;
+    unsigned page, slot;
     if (ps_shift >= 0) {
-      page = j >> ps_shift;
-      slot = j & (PS - 1);
+      page = (unsigned)j >> ps_shift;
+      slot = (unsigned)j & (unsigned)(PS - 1);
     } else {
-      page = j / PS;
-      slot = j - page * PS;
+      page = (unsigned)j / (unsigned)PS;
+      slot = (unsigned)j - page * (unsigned)PS;
     }
-    if (page >= max_blocks) return -1;
-    int phi;
+    if (page >= (unsigned)max_blocks) return -1;
+    unsigned nb, pp;
     if (block_table != nullptr) {
-      phi = block_table[(int64_t)b * max_blocks + page];
-      if (phi < 0 || phi >= num_phys) return -1;
+      typedef const __attribute__((address_space(4))) int32_t ctable;
+      const int phi = ((ctable*)block_table)[(int64_t)b * max_blocks + page];
+      if ((unsigned)phi >= (unsigned)num_phys) return -1;
+      if (num_phys <= P) {
+        nb = 0;
+        pp = (unsigned)phi;
+      } else {
+        nb = (unsigned)phi / (unsigned)P;
+        pp = (unsigned)phi - nb * (unsigned)P;
+      }
     } else {
-      phi = b * P + page;
+      nb = (unsigned)b;
+      pp = page;
     }
-    int nb = phi / P;
-    int pp = phi - nb * P;
     return (int64_t)nb * stride_nb + (int64_t)hk * stride_hk + (int64_t)pp * stride_page +
            (int64_t)slot * D;
   }

@@ -25,6 +25,8 @@
 //    rows start first.
 #include "fa_common.h"
 
+#include <type_traits>
+
 namespace fa {
 
 namespace {
@@ -331,6 +333,8 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
 constexpr float kRescaleLog2 = 8.f;
 
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            (int)kRsrcWord3);
@@ -352,34 +356,79 @@ struct DmaCfg {
   __device__ static int swz_v(int row) { return (4 * row) % CH; }
 };
 
-// Issue the DMA of one 64-key tile (wave w moves keys k0+16w .. +15).
+// Page part of one tile DMA: this wave's 16-key quarter (keys k0+16w ..)
+// lies in one page; `off` is its element offset (0 when nothing is valid)
+// and `nbytes` the bytes of its valid rows (the buffer range: rows beyond
+// read as zero).
+struct QuarterSrc {
+  int64_t off;
+  uint32_t nbytes;
+};
+
 template <int D>
-__device__ __forceinline__ void dma_tile(const AttnParams& p, const char* kp, const char* vp,
-                                         int b, int hk, int k0, int kv_len, int wave, int lane,
-                                         char* sK, char* sV) {
+__device__ __forceinline__ QuarterSrc quarter_src(const AttnParams& p, int b, int hk, int k0,
+                                                  int kv_len, int wave) {
   using C = DmaCfg<D>;
   const int g0 = k0 + 16 * wave;
   const int valid = min(16, kv_len - g0);
-  int64_t off = 0;
-  uint32_t nbytes = 0;
+  QuarterSrc q{0, 0u};
   if (valid > 0) {
-    off = p.kv.row_offset(b, hk, g0);
-    nbytes = off >= 0 ? (uint32_t)(valid * C::ROWB) : 0u;
-    off = off >= 0 ? off : 0;
+    const int64_t off = p.kv.row_offset(b, hk, g0);
+    if (off >= 0) q = QuarterSrc{off, (uint32_t)(valid * C::ROWB)};
   }
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + off * 2, nbytes);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + off * 2, nbytes);
+  return q;
+}
+
+// Per-lane byte offsets of the DMA within a quarter (loop invariant).
+template <int D>
+struct DmaLane {
+  uint32_t vk[DmaCfg<D>::IPQ];
+  uint32_t vv[DmaCfg<D>::IPQ];
+};
+
+template <int D>
+__device__ __forceinline__ DmaLane<D> dma_lane(int wave, int lane) {
+  using C = DmaCfg<D>;
+  DmaLane<D> d;
   const int pch = lane % C::CH;
 #pragma unroll
   for (int i = 0; i < C::IPQ; ++i) {
     const int rq = C::RPI * i + lane / C::CH;  // row within the quarter
     const int rt = 16 * wave + rq;             // row within the tile
-    const uint32_t vk = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_k(rt)));
-    const uint32_t vv = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_v(rt)));
-    const int dst = (16 * wave + C::RPI * i) * C::ROWB;  // 1 KB block of rows rt - rq + RPI*i
-    lds_dma16(rk, sK + dst, vk);
-    lds_dma16(rv, sV + dst, vv);
+    d.vk[i] = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_k(rt)));
+    d.vv[i] = (uint32_t)(rq * C::ROWB + 16 * (pch ^ C::swz_v(rt)));
   }
+  return d;
+}
+
+// Issue the DMA of one 64-key tile (wave w moves keys k0+16w .. +15).
+template <int D>
+__device__ __forceinline__ void dma_tile(const QuarterSrc& q, const DmaLane<D>& dl,
+                                         const char* kp, const char* vp, int wave, char* sK,
+                                         char* sV) {
+  using C = DmaCfg<D>;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + q.off * 2, q.nbytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + q.off * 2, q.nbytes);
+#pragma unroll
+  for (int i = 0; i < C::IPQ; ++i) {
+    const int dst = (16 * wave + C::RPI * i) * C::ROWB;  // 1 KB block of the quarter
+    lds_dma16(rk, sK + dst, dl.vk[i]);
+    lds_dma16(rv, sV + dst, dl.vv[i]);
+  }
+}
+
+// V^T operand (8 keys of one d per lane) of PV step s, d block i, via two
+// transposing reads; voff holds the lane's byte offset within the K|V pair.
+template <int D>
+__device__ __forceinline__ half8 ld_vt(const char* buf, const int* voff, int s, int i) {
+  using C = DmaCfg<D>;
+  const char* va = buf + voff[i] + 16 * s * C::ROWB;
+  const half4 lo = __builtin_bit_cast(
+      half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(va)));
+  const half4 hi = __builtin_bit_cast(
+      half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                 (__attribute__((address_space(3))) short4v*)(va + 8 * C::ROWB)));
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 template <int D>
@@ -436,7 +485,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, 
 
   const char* kp = reinterpret_cast<const char*>(p.k);
   const char* vp = reinterpret_cast<const char*>(p.v);
-  if (ntiles > 0) dma_tile<D>(p, kp, vp, b, hk, 0, kv_len, wave, lane, smem, smem + C::TILE);
+  const DmaLane<D> dl = dma_lane<D>(wave, lane);
+  if (ntiles > 0)
+    dma_tile<D>(quarter_src<D>(p, b, hk, 0, kv_len, wave), dl, kp, vp, wave, smem, smem + C::TILE);
+  // Page of the next tile to fetch, looked up one iteration before its DMA.
+  QuarterSrc next_src = quarter_src<D>(p, b, hk, kBN, kv_len, wave);
 
   const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
   half8 qreg[KSTEPS];
@@ -470,26 +523,48 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, 
   float m_ref = -INFINITY;  // scaled (log2) reference max
   float l_run = 0.f;
   const float c = p.scale_log2;
+  const half2v ones = half2v{(f16)1.f, (f16)1.f};
 
-  for (int t = 0; t < ntiles; ++t) {
+  // Iteration t computes tile t from buffer t&1 and prefetches tile t+1 into
+  // the other buffer; unrolled by two so buffer offsets are immediates.
+  auto step = [&](auto par, int t) {
+    constexpr int PB = decltype(par)::value;  // t & 1
     const int k0 = t * kBN;
-    char* buf = smem + (t & 1) * 2 * C::TILE;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t + 1 < ntiles) {
-      char* nbuf = smem + ((t + 1) & 1) * 2 * C::TILE;
-      dma_tile<D>(p, kp, vp, b, hk, k0 + kBN, kv_len, wave, lane, nbuf, nbuf + C::TILE);
+      char* nbuf = smem + (PB ^ 1) * 2 * C::TILE;
+      dma_tile<D>(next_src, dl, kp, vp, wave, nbuf, nbuf + C::TILE);
+      next_src = quarter_src<D>(p, b, hk, k0 + 2 * kBN, kv_len, wave);
     }
-    if (k0 >= wave_lim_max) continue;
+    if (k0 >= wave_lim_max) return;
+    const char* buf = smem + PB * 2 * C::TILE;
 
+    // S^T: K operands are read KA k-steps ahead of their MFMAs.
+    constexpr int KA = 2;
     floatx16 s0 = floatx16{}, s1 = floatx16{};
+    half8 ka[KA][2];
+#pragma unroll
+    for (int i = 0; i < KA; ++i) {
+      ka[i][0] = *reinterpret_cast<const half8*>(buf + koff[i]);
+      ka[i][1] = *reinterpret_cast<const half8*>(buf + koff[i] + 32 * C::ROWB);
+    }
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      const half8 a0 = *reinterpret_cast<const half8*>(buf + koff[ks]);
-      const half8 a1 = *reinterpret_cast<const half8*>(buf + koff[ks] + 32 * C::ROWB);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % KA][0], qreg[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % KA][1], qreg[ks], s1, 0, 0, 0);
+      if (ks + KA < KSTEPS) {
+        ka[ks % KA][0] = *reinterpret_cast<const half8*>(buf + koff[ks + KA]);
+        ka[ks % KA][1] = *reinterpret_cast<const half8*>(buf + koff[ks + KA] + 32 * C::ROWB);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // First V^T operands of the PV product, in flight during the softmax.
+    constexpr int NMF = 4 * DBLK;  // PV MFMAs per tile: (16-key step, d block)
+    constexpr int VA = 3;
+    half8 va[VA];
+#pragma unroll
+    for (int m = 0; m < VA; ++m) va[m] = ld_vt<D>(buf, voff, m / DBLK, m % DBLK);
     if (k0 + kBN > wave_lim_min) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -498,9 +573,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, 
         if (key + 32 >= lim) s1[r] = -INFINITY;
       }
     }
-    float mx = -INFINITY;
+    float mx = max3f(s0[0], s0[1], s0[2]);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    for (int r = 3; r < 15; r += 2) mx = max3f(mx, s0[r], s0[r + 1]);
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) mx = max3f(mx, s1[r], s1[r + 1]);
+    mx = fmaxf(mx, s0[15]);
     mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
     if (__builtin_amdgcn_ballot_w64(mx > m_ref + kRescaleLog2) != 0) {
       const float m_new = fmaxf(m_ref, mx);
@@ -511,37 +589,36 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, 
       m_ref = m_new;
     }
     const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -m_use));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -m_use));
-      psum += s0[r] + s1[r];
-    }
-    l_run += psum;
+    // P^T operands of the four 16-key steps, and their row sum from the same
+    // fp16 values the PV product uses.
     half8 pb[4];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      pb[0][j] = (f16)s0[j];
-      pb[1][j] = (f16)s0[8 + j];
-      pb[2][j] = (f16)s1[j];
-      pb[3][j] = (f16)s1[8 + j];
+      pb[0][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[j], c, -m_use));
+      pb[1][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[8 + j], c, -m_use));
+      pb[2][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s1[j], c, -m_use));
+      pb[3][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s1[8 + j], c, -m_use));
     }
+    float psum = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int i = 0; i < DBLK; ++i) {
-        const char* va = buf + voff[i] + 16 * s * C::ROWB;
-        const half4 lo = __builtin_bit_cast(
-            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                       (__attribute__((address_space(3))) short4v*)(va)));
-        const half4 hi = __builtin_bit_cast(
-            half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                       (__attribute__((address_space(3))) short4v*)(va + 8 * C::ROWB)));
-        const half8 a = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[s], acc_o[i], 0, 0, 0);
-      }
+      for (int j = 0; j < 8; j += 2)
+        psum = __builtin_amdgcn_fdot2(half2v{pb[s][j], pb[s][j + 1]}, ones, psum, false);
     }
+    l_run += psum;
+    // O^T += V^T P^T: operands read VA MFMAs ahead.
+#pragma unroll
+    for (int m = 0; m < NMF; ++m) {
+      const int st = m / DBLK, i = m % DBLK;
+      acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[m % VA], pb[st], acc_o[i], 0, 0, 0);
+      if (m + VA < NMF) va[m % VA] = ld_vt<D>(buf, voff, (m + VA) / DBLK, (m + VA) % DBLK);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < ntiles) step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   if (qrow >= p.M) return;
