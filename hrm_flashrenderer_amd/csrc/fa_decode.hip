@@ -23,8 +23,10 @@
 //    consecutive d each (whole 256-byte rows across a quarter-wave), and the
 //    d index of the MFMA output is relabelled d = (D/16)*m + j so that the
 //    transpose is a byte permute inside the lane.
-//  * Partial (max, sum, O) of each split go to a workspace; a combine kernel
-//    merges the splits of a row in log2 space.
+//  * Each wave keeps a per-row reference max in log2 units (scores times
+//    log2(e)/sqrt(D)) and rescales O only when a group's max exceeds it by more
+//    than 2^8. Partial (max, sum, O) of each split go to a workspace; a combine
+//    kernel merges the splits of a row in log2 space.
 #include "fa_common.h"
 
 #include <stdlib.h>
@@ -202,79 +204,87 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams
       }
     }
 
-    float m_run = -INFINITY;
+    float m_ref = -INFINITY;  // scaled (log2) reference max of the row
     float l_run = 0.f;
+    const half2v ones = half2v{(f16)1.f, (f16)1.f};
     floatx4 acc_o[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    int g = g_begin + wave;
-    DecodeRegs<D> cur;
-    if (g < g_end) load_group<D, ALIGNED>(cur, p, kp, vp, b, hk, g << 4, t_end, n, quarter);
-    while (g < g_end) {
-      const int t0 = g << 4;
-      const int g_next = g + kDecodeWaves;
-      DecodeRegs<D> nxt;
-      if (g_next < g_end)
-        load_group<D, ALIGNED>(nxt, p, kp, vp, b, hk, g_next << 4, t_end, n, quarter);
-
-      // S^T[token][row] for the 16 tokens of the group.
+    // One 16-token group: S^T on the matrix cores, online softmax with a lazy
+    // reference max (O is rescaled only when the max grows by more than 2^8),
+    // then O^T += V^T P^T with the in-lane V transpose.
+    auto process = [&](const DecodeRegs<D>& r, int t0) {
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KSTEPS; ++kk) {
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, cur.k[kk]), qreg[kk],
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qreg[kk],
                                                    s, 0, 0, 0);
       }
-      // lane holds tokens t0 + 4*quarter + r of row n
+      // lane holds tokens t0 + 4*quarter + i of row n
       float sv[4];
-      float gmax = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = t0 + 4 * quarter + r;
-        sv[r] = tok < row_lim ? s[r] : -INFINITY;
-        gmax = fmaxf(gmax, sv[r]);
-      }
-      gmax = wave_max16x(gmax);
-      const float m_new = fmaxf(m_run, gmax);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
-      const float mc = m_use * c;
-      float pr[4];
-      float psum = 0.f;
+      for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim ? s[i] : -INFINITY;
+      const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
+      if (__builtin_amdgcn_ballot_w64(gmax > m_ref + 8.f) != 0) {
+        const float m_new = fmaxf(m_ref, gmax);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], c, -mc));
-        psum += pr[r];
+        for (int j = 0; j < DPL; ++j) acc_o[j] = acc_o[j] * alpha;
+        m_ref = m_new;
       }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      const half4 pb = half4{(f16)pr[0], (f16)pr[1], (f16)pr[2], (f16)pr[3]};
-
+      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+      half4 pb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, -m_use));
+      l_run = __builtin_amdgcn_fdot2(half2v{pb[0], pb[1]}, ones, l_run, false);
+      l_run = __builtin_amdgcn_fdot2(half2v{pb[2], pb[3]}, ones, l_run, false);
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
         const int w = j >> 1;
         uint32_t lo, hi;
         if ((j & 1) == 0) {
-          lo = pack_lo(cur.v[0][w], cur.v[1][w]);
-          hi = pack_lo(cur.v[2][w], cur.v[3][w]);
+          lo = pack_lo(r.v[0][w], r.v[1][w]);
+          hi = pack_lo(r.v[2][w], r.v[3][w]);
         } else {
-          lo = pack_hi(cur.v[0][w], cur.v[1][w]);
-          hi = pack_hi(cur.v[2][w], cur.v[3][w]);
+          lo = pack_hi(r.v[0][w], r.v[1][w]);
+          hi = pack_hi(r.v[2][w], r.v[3][w]);
         }
         const half4 a = __builtin_bit_cast(half4, u32x2{lo, hi});
-        acc_o[j] = acc_o[j] * alpha;
         acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc_o[j], 0, 0, 0);
       }
-      (void)VW;
-      cur = nxt;
-      g = g_next;
+    };
+
+    // Groups g_begin + wave + 4k of the split, through a ring of RING register
+    // sets: RING - 1 groups are in flight while one is processed.
+    constexpr int RING = 3;
+    DecodeRegs<D> ring[RING];
+    const int g0 = g_begin + wave;
+#pragma unroll
+    for (int i = 0; i < RING - 1; ++i) {
+      const int gi = g0 + i * kDecodeWaves;
+      if (gi < g_end) load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter);
     }
+    for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
+#pragma unroll
+      for (int i = 0; i < RING; ++i) {
+        const int gi = g + i * kDecodeWaves;
+        if (gi >= g_end) break;
+        const int gl = gi + (RING - 1) * kDecodeWaves;
+        if (gl < g_end)
+          load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
+                                 quarter);
+        process(ring[i], gi << 4);
+      }
+    }
+    (void)VW;
 
     // Merge the 4 waves' states in LDS: m is uniform per row, l needs the
     // 4 lanes of a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j.
     l_run = wave_sum16x(l_run);
     if (quarter == 0) {
-      s_m[wave][n] = m_run;
+      s_m[wave][n] = m_ref;
       s_l[wave][n] = l_run;
     }
 #pragma unroll
@@ -296,7 +306,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams
       if (mx != -INFINITY) {
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; ++w) {
-          const float sc = __builtin_amdgcn_exp2f((s_m[w][row] - mx) * c);
+          const float sc = __builtin_amdgcn_exp2f(s_m[w][row] - mx);
           lsum += sc * s_l[w][row];
           osum += sc * s_o[w][row][d];
         }
@@ -354,9 +364,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
     if (mx != -INFINITY) {
-      const float c = p.scale_log2;
       for (int s = 0; s < nsp; ++s) {
-        const float sc = __builtin_amdgcn_exp2f((p.ws_ml[(slot0 + s) * 2] - mx) * c);
+        const float sc = __builtin_amdgcn_exp2f(p.ws_ml[(slot0 + s) * 2] - mx);
         lsum += sc * p.ws_ml[(slot0 + s) * 2 + 1];
 #pragma unroll
         for (int k = 0; k < DPW; ++k) acc[k] += sc * p.ws_o[(slot0 + s) * D + lane + 64 * k];
