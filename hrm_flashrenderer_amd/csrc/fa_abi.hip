@@ -140,7 +140,7 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacity_pages,
                                 int page_size) {
   if (B <= 0 || Hq <= 0 || M <= 0 || Hk <= 0 || !head_dim_ok(D)) return 0;
-  if (!fa::use_decode_path(M, Hq, Hk)) return 0;
+  if (!fa::use_decode_path(B, M, Hq, Hk)) return 0;
   const int cap = capacity_tokens(capacity_pages < 0 ? 0 : capacity_pages,
                                   page_size < 1 ? 1 : page_size);
   return fa::plan_decode(B, Hq, M, D, Hk, cap).ws_bytes;
@@ -184,17 +184,17 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
   p.scale_log2 = fa::kLog2e / sqrtf((float)D);
 
   (void)hipGetLastError();
-  if (fa::use_decode_path(M, Hq, Hk)) {
+  if (fa::use_decode_path(B, M, Hq, Hk)) {
     const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N);
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
                   workspace == nullptr ? (size_t)0 : workspace_bytes);
-    const size_t slots = (size_t)B * Hq * M * plan.nsplit;
-    const size_t o_bytes = ((slots * D * sizeof(float)) + 255) / 256 * 256;
-    p.ws_o = reinterpret_cast<float*>(workspace);
-    p.ws_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + o_bytes);
-    p.nsplit = plan.nsplit;
-    p.split_tokens = plan.split_tokens;
+    char* ws = reinterpret_cast<char*>(workspace);
+    p.ws_o = reinterpret_cast<float*>(ws);
+    p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
+    p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
+    p.dec_wgs = plan.wgs;
+    p.dec_rows = plan.rows;
     return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
   }
   return launch_status(fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream));

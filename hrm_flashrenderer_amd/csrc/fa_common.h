@@ -95,11 +95,13 @@ struct AttnParams {
   int causal;
   int q_offset, k_offset;
   float scale_log2;     // log2(e) / sqrt(D)
-  // split-K decode scratch
-  float* ws_o;          // [B, Hq, M, nsplit, D]
-  float* ws_ml;         // [B, Hq, M, nsplit, 2]
-  int nsplit;
-  int split_tokens;
+  // balanced decode scratch: partial results of (segment, workgroup) pairs at
+  // slot = segment + workgroup, segment = b*Hk + hk (see fa_decode.hip)
+  float* ws_o;          // [B*Hk + dec_wgs, dec_rows, D]
+  float* ws_ml;         // [B*Hk + dec_wgs, dec_rows, 2]  (log2 max, sum)
+  int* ws_units;        // [B + 1] units (16-key groups x Hk) before sequence b
+  int dec_wgs;          // workgroups of the decode kernel
+  int dec_rows;         // row capacity of a slot: Hq * M
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
@@ -125,13 +127,15 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream);
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
 
-// Split-K sizing of the decode path (host side; depends on sizes only).
+// Decode sizing (host side; depends on sizes only).
 struct DecodePlan {
-  int nsplit;
-  int split_tokens;
-  size_t ws_bytes;
+  int wgs;          // workgroups sharing the work evenly
+  int rows;         // row capacity of a partial slot
+  size_t o_bytes;   // partial O, 256-byte aligned
+  size_t ml_bytes;  // partial (max, sum), 256-byte aligned
+  size_t ws_bytes;  // total, including the unit prefix
 };
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
-bool use_decode_path(int M, int Hq, int Hk);
+bool use_decode_path(int B, int M, int Hq, int Hk);
 
 }  // namespace fa

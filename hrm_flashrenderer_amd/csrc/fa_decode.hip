@@ -7,13 +7,17 @@
 // (flashattention_custom/ops.py:37-63, csrc/flash_attn_sm75.cu:213-425).
 //
 // Design (HBM-bound; every K/V byte is read once per KV head):
-//  * One workgroup = (split of the context, KV head hk, sequence b). It serves
-//    every query row that reads hk: all q heads of the GQA group times the M
-//    query positions, packed as the 16 columns of the MFMA tiles. K/V pages are
-//    therefore read once per KV head, not once per query head.
-//  * The split's tokens are walked in 16-token groups; the 4 waves take groups
-//    round-robin and keep their own running (max, sum, O) state; the next
-//    group's K/V are loaded into registers before the current one is used.
+//  * The work is split evenly: the (sequence, KV head, 16-token group) units
+//    of the whole batch are counted on the device from seqlen, and each of W
+//    workgroups takes an equal contiguous range (see decode_kernel), so
+//    variable context lengths leave no tail and no idle workgroups.
+//  * A workgroup serves every query row that reads its KV head: all q heads of
+//    the GQA group times the M query positions, packed as the 16 columns of
+//    the MFMA tiles. K/V pages are therefore read once per KV head, not once
+//    per query head.
+//  * The segment's groups are dealt round-robin to the 4 waves, each keeping
+//    its own running (max, sum, O) state and two groups in flight ahead of
+//    the one it computes.
 //  * S^T = K Q^T with v_mfma_f32_16x16x32_f16: lane (n, quarter) loads K row
 //    n of the group as 16-byte vectors straight from HBM (no LDS). The
 //    accumulator gives each lane 4 tokens of one query row, which is exactly
@@ -25,11 +29,13 @@
 //    transpose is a byte permute inside the lane.
 //  * Each wave keeps a per-row reference max in log2 units (scores times
 //    log2(e)/sqrt(D)) and rescales O only when a group's max exceeds it by more
-//    than 2^8. Partial (max, sum, O) of each split go to a workspace; a combine
-//    kernel merges the splits of a row in log2 space.
+//    than 2^8. Partial (max, sum, O) of each (segment, workgroup) go to a
+//    workspace; a combine kernel merges the partials of a row in log2 space.
 #include "fa_common.h"
 
 #include <stdlib.h>
+
+#include <algorithm>
 
 namespace fa {
 
@@ -39,6 +45,7 @@ constexpr int kDecodeThreads = 256;  // 4 waves
 constexpr int kDecodeWaves = 4;
 constexpr int kRows = 16;            // query rows per MFMA column block
 constexpr int kMaxHeads = 256;       // q heads scanned per KV head
+constexpr int kMaxBatch = 2048;      // sequences whose unit prefix fits in LDS
 
 __device__ __forceinline__ float wave_max16x(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
@@ -69,31 +76,65 @@ struct DecodeRegs {
   uint32_t v[4][VW];
 };
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);  // raw buffer, dword format (gfx9)
+}
+
+// Per-lane byte offsets of a group's fragments inside its page (loop invariant):
+// K row n, 16-byte chunks 2*quarter + 4*kk; V rows 4*quarter + i, DPL halves at DPL*n.
+template <int D>
+struct GroupLane {
+  uint32_t k;
+  uint32_t v;
+  __device__ GroupLane(int n, int quarter)
+      : k((uint32_t)(n * 2 * D + 16 * quarter)),
+        v((uint32_t)(4 * quarter * 2 * D + 2 * (D / 16) * n)) {}
+};
+
 // Loads the K/V fragments of one 16-token group (rows beyond `t_end` or not
 // addressable read as zero, so masked keys never carry NaN garbage into P V).
 // ALIGNED (pages of a multiple of 16 tokens, or contiguous K/V): the group sits
-// in one page, found by one wave-uniform (scalar) block-table read, so no
-// vector-memory wait separates the group's loads from the ones in flight.
+// in one page, found by one wave-uniform (scalar) lookup; the loads are raw
+// buffer loads from that page whose range covers only the group's valid rows,
+// so rows past t_end come back as zeros with no per-lane address math.
 template <int D, bool ALIGNED>
 __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p, const f16* kp,
                                            const f16* vp, int b, int hk, int t0, int t_end,
-                                           int n, int quarter) {
+                                           int n, int quarter, const GroupLane<D>& gl) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
   constexpr int VW = DecodeRegs<D>::VW;
-  int64_t gbase = -1;
-  if constexpr (ALIGNED) gbase = p.kv.row_offset(b, hk, t0);  // t0 < t_end <= capacity
-  auto row_off = [&](int row) -> int64_t {
-    if (row >= t_end) return -1;
-    if constexpr (ALIGNED) {
-      return gbase < 0 ? -1 : gbase + (int64_t)(row - t0) * D;
-    } else {
-      return p.kv.row_offset(b, hk, row);
+  if constexpr (ALIGNED) {
+    // A group at or past t_end gets an empty range: its loads are issued (so
+    // the count of loads in flight does not depend on the path) but touch no
+    // memory and return zeros.
+    const int valid = min(16, t_end - t0);
+    int64_t off = valid > 0 ? p.kv.row_offset(b, hk, t0) : -1;
+    const uint32_t nbytes = off >= 0 ? (uint32_t)(valid * 2 * D) : 0u;
+    off = off >= 0 ? off : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + off, nbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + off, nbytes);
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      r.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, gl.k + 64 * kk, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (VW == 4) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, gl.v + i * 2 * D, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r.v[i][w] = x[w];
+      } else {
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, gl.v + i * 2 * D, 0, 0);
+#pragma unroll
+        for (int w = 0; w < VW; ++w) r.v[i][w] = x[w];
+      }
     }
-  };
+    return;
+  }
   {
     const int row = t0 + n;
-    const int64_t off = row_off(row);
+    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
       if (off >= 0) {
@@ -106,7 +147,7 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = t0 + 4 * quarter + i;
-    const int64_t off = row_off(row);
+    const int64_t off = row < t_end ? p.kv.row_offset(b, hk, row) : -1;
     if constexpr (VW == 4) {
       u32x4 x = u32x4{0u, 0u, 0u, 0u};
       if (off >= 0) x = *reinterpret_cast<const u32x4*>(vp + off + DPL * n);
@@ -121,8 +162,51 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
   }
 }
 
+// Groups (16 keys) of sequence b that some query row can see.
+__device__ __forceinline__ int visible_groups(const AttnParams& p, int b) {
+  int kv_lim = p.kv_len(b);
+  if (p.causal) {
+    const int64_t lim = (int64_t)p.q_off(b) + (p.M - 1) - p.k_off(b) + 1;
+    if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
+  }
+  return kv_lim > 0 ? (kv_lim + 15) >> 4 : 0;
+}
+
+// s_units[b] = Hk * (visible groups of sequences before b), s_units[B] = total,
+// computed by the whole workgroup (chunked sums + a 256-wide scan).
+__device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, int* s_part) {
+  const int tid = threadIdx.x;
+  const int chunk = (p.B + kDecodeThreads - 1) / kDecodeThreads;
+  const int b0 = tid * chunk, b1 = min(p.B, b0 + chunk);
+  int sum = 0;
+  for (int b = b0; b < b1; ++b) sum += visible_groups(p, b) * p.Hk;
+  s_part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kDecodeThreads; off <<= 1) {
+    const int v = tid >= off ? s_part[tid - off] : 0;
+    __syncthreads();
+    s_part[tid] += v;
+    __syncthreads();
+  }
+  int run = tid > 0 ? s_part[tid - 1] : 0;
+  for (int b = b0; b < b1; ++b) {
+    s_units[b] = run;
+    run += visible_groups(p, b) * p.Hk;
+  }
+  if (tid == kDecodeThreads - 1) s_units[p.B] = s_part[kDecodeThreads - 1];
+  __syncthreads();
+}
+
+// Balanced decode. The work is the list of units (sequence b, KV head hk,
+// 16-key group g) in (b, hk, g) order; workgroup w of W takes units
+// [w*U/W, (w+1)*U/W), i.e. an equal share whatever the sequence lengths. It
+// walks the (b, hk) segments of its range; for each it runs all query rows
+// of hk over its groups and writes one partial (max, sum, O) per row at slot
+// b*Hk + hk + w. Along the unit list both the segment and the workgroup
+// index are non-decreasing and at least one grows at every change, so
+// segment + workgroup is unique per (segment, workgroup) pair.
 template <int D, bool ALIGNED>
-__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams p) {
+__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
   constexpr int VW = DecodeRegs<D>::VW;
@@ -130,201 +214,234 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(AttnParams
 
   __shared__ int s_heads[kMaxHeads];
   __shared__ int s_count;
+  __shared__ int s_units[kMaxBatch + 1];
+  __shared__ int s_part[kDecodeThreads];
   __shared__ float s_m[kDecodeWaves][kRows];
   __shared__ float s_l[kDecodeWaves][kRows];
   __shared__ float s_o[kDecodeWaves][kRows][OPAD];
 
-  const int split = blockIdx.x;
-  const int hk = blockIdx.y;
-  const int b = blockIdx.z;
+  const int w = blockIdx.x;
+  const int W = gridDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;       // MFMA column: query row within the block
   const int quarter = lane >> 4; // 0..3
 
-  const int kv_len = p.kv_len(b);
-  const int qo = p.q_off(b);
-  const int ko = p.k_off(b);
-  int kv_lim = kv_len;
-  if (p.causal) {
-    int64_t lim = (int64_t)qo + (p.M - 1) - ko + 1;
-    if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
+  unit_prefix(p, s_units, s_part);
+  const int U = s_units[p.B];
+  if (w == 0) {
+    for (int b = tid; b <= p.B; b += kDecodeThreads) p.ws_units[b] = s_units[b];
   }
-  const int t_begin = split * p.split_tokens;
-  if (t_begin >= kv_lim) return;  // the combine kernel skips this split
-  const int t_end = min(kv_lim, t_begin + p.split_tokens);
-
-  // Query heads that read KV head hk (any head_map, not only h / group).
-  if (wave == 0) {
-    int count = 0;
-    for (int base = 0; base < p.Hq; base += 64) {
-      const int hq = base + lane;
-      const bool match = hq < p.Hq && p.kv_head(hq) == hk;
-      const uint64_t mask = __ballot(match);
-      if (match) {
-        const int pos = count + __popcll(mask & ((1ull << lane) - 1ull));
-        if (pos < kMaxHeads) s_heads[pos] = hq;
-      }
-      count += __popcll(mask);
-    }
-    if (lane == 0) s_count = min(count, kMaxHeads);
-  }
-  __syncthreads();
-  const int nrows = s_count * p.M;
+  const int u0 = (int)((int64_t)w * U / W);
+  const int u1 = (int)((int64_t)(w + 1) * U / W);
+  if (u0 >= u1) return;
 
   const f16* qp = reinterpret_cast<const f16*>(p.q);
   const f16* kp = reinterpret_cast<const f16*>(p.k);
   const f16* vp = reinterpret_cast<const f16*>(p.v);
   const float c = p.scale_log2;
 
-  const int g_begin = t_begin >> 4;
-  const int g_end = (t_end + 15) >> 4;
-
-  for (int rc = 0; rc < nrows; rc += kRows) {
-    // This lane's query row (column n of the tiles).
-    const int ridx = rc + n;
-    const bool row_ok = ridx < nrows;
-    const int hq = row_ok ? s_heads[ridx / p.M] : 0;
-    const int qi = row_ok ? ridx % p.M : 0;
-    int row_lim = t_end;  // keys j < row_lim are visible to this row
+  // One (b, hk) segment, groups [g_begin, g_end).
+  auto segment = [&](int b, int hk, int g_begin, int g_stop, int slot) {
+    const int kv_len = p.kv_len(b);
+    const int qo = p.q_off(b);
+    const int ko = p.k_off(b);
+    int kv_lim = kv_len;
     if (p.causal) {
-      int64_t lim = (int64_t)qo + qi - ko + 1;
-      if (lim < row_lim) row_lim = lim < 0 ? 0 : (int)lim;
+      int64_t lim = (int64_t)qo + (p.M - 1) - ko + 1;
+      if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
     }
+    const int t_end = min(kv_lim, g_stop << 4);
+    const int g_end = g_stop;
 
-    half8 qreg[KSTEPS];
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      if (row_ok) {
-        const int64_t qoff = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 32 * kk + 8 * quarter;
-        qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
-      } else {
-        qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    // Query heads that read KV head hk (any head_map, not only h / group).
+    if (wave == 0) {
+      int count = 0;
+      for (int base = 0; base < p.Hq; base += 64) {
+        const int hq = base + lane;
+        const bool match = hq < p.Hq && p.kv_head(hq) == hk;
+        const uint64_t mask = __ballot(match);
+        if (match) {
+          const int pos = count + __popcll(mask & ((1ull << lane) - 1ull));
+          if (pos < kMaxHeads) s_heads[pos] = hq;
+        }
+        count += __popcll(mask);
       }
+      if (lane == 0) s_count = min(count, kMaxHeads);
     }
+    __syncthreads();
+    const int nrows = s_count * p.M;
 
-    float m_ref = -INFINITY;  // scaled (log2) reference max of the row
-    float l_run = 0.f;
-    const half2v ones = half2v{(f16)1.f, (f16)1.f};
-    floatx4 acc_o[DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int rc = 0; rc < nrows; rc += kRows) {
+      // This lane's query row (column n of the tiles).
+      const int ridx = rc + n;
+      const bool row_ok = ridx < nrows;
+      const int hq = row_ok ? s_heads[ridx / p.M] : 0;
+      const int qi = row_ok ? ridx % p.M : 0;
+      int row_lim = t_end;  // keys j < row_lim are visible to this row
+      if (p.causal) {
+        int64_t lim = (int64_t)qo + qi - ko + 1;
+        if (lim < row_lim) row_lim = lim < 0 ? 0 : (int)lim;
+      }
 
-    // One 16-token group: S^T on the matrix cores, online softmax with a lazy
-    // reference max (O is rescaled only when the max grows by more than 2^8),
-    // then O^T += V^T P^T with the in-lane V transpose.
-    auto process = [&](const DecodeRegs<D>& r, int t0) {
-      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+      half8 qreg[KSTEPS];
 #pragma unroll
       for (int kk = 0; kk < KSTEPS; ++kk) {
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qreg[kk],
-                                                   s, 0, 0, 0);
+        if (row_ok) {
+          const int64_t qoff = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 32 * kk + 8 * quarter;
+          qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
+        } else {
+          qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
       }
-      // lane holds tokens t0 + 4*quarter + i of row n
-      float sv[4];
+
+      float m_ref = -INFINITY;  // scaled (log2) reference max of the row
+      float l_run = 0.f;
+      const half2v ones = half2v{(f16)1.f, (f16)1.f};
+      floatx4 acc_o[DPL];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim ? s[i] : -INFINITY;
-      const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
-      if (__builtin_amdgcn_ballot_w64(gmax > m_ref + 8.f) != 0) {
-        const float m_new = fmaxf(m_ref, gmax);
-        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-        l_run *= alpha;
+      for (int j = 0; j < DPL; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+      // One 16-token group: S^T on the matrix cores, online softmax with a lazy
+      // reference max (O is rescaled only when the max grows by more than 2^8),
+      // then O^T += V^T P^T with the in-lane V transpose.
+      auto process = [&](const DecodeRegs<D>& r, int t0) {
+        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc_o[j] = acc_o[j] * alpha;
-        m_ref = m_new;
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qreg[kk],
+                                                     s, 0, 0, 0);
+        }
+        // lane holds tokens t0 + 4*quarter + i of row n
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim ? s[i] : -INFINITY;
+        const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
+        if (__builtin_amdgcn_ballot_w64(gmax > m_ref + 8.f) != 0) {
+          const float m_new = fmaxf(m_ref, gmax);
+          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+          l_run *= alpha;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc_o[j] = acc_o[j] * alpha;
+          m_ref = m_new;
+        }
+        const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+        half4 pb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, -m_use));
+        l_run = __builtin_amdgcn_fdot2(half2v{pb[0], pb[1]}, ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2(half2v{pb[2], pb[3]}, ones, l_run, false);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int w = j >> 1;
+          uint32_t lo, hi;
+          if ((j & 1) == 0) {
+            lo = pack_lo(r.v[0][w], r.v[1][w]);
+            hi = pack_lo(r.v[2][w], r.v[3][w]);
+          } else {
+            lo = pack_hi(r.v[0][w], r.v[1][w]);
+            hi = pack_hi(r.v[2][w], r.v[3][w]);
+          }
+          const half4 a = __builtin_bit_cast(half4, u32x2{lo, hi});
+          acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc_o[j], 0, 0, 0);
+        }
+      };
+
+      // Groups g_begin + wave + 4k of the segment, through a ring of RING register
+      // sets: RING - 1 groups are in flight while one is processed.
+      constexpr int RING = 3;
+      DecodeRegs<D> ring[RING];
+      const GroupLane<D> glane(n, quarter);
+      const int g0 = g_begin + wave;
+      // With ALIGNED loads every prefetch is issued unconditionally (groups past
+      // the end read as empty ranges), which keeps the number of loads in flight
+      // the same on every path, so each group waits only for its own loads.
+#pragma unroll
+      for (int i = 0; i < RING - 1; ++i) {
+        const int gi = g0 + i * kDecodeWaves;
+        if (ALIGNED || gi < g_end)
+          load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter, glane);
       }
-      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-      half4 pb;
+      for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, -m_use));
-      l_run = __builtin_amdgcn_fdot2(half2v{pb[0], pb[1]}, ones, l_run, false);
-      l_run = __builtin_amdgcn_fdot2(half2v{pb[2], pb[3]}, ones, l_run, false);
+        for (int i = 0; i < RING; ++i) {
+          const int gi = g + i * kDecodeWaves;
+          if (gi >= g_end) break;
+          const int gl = gi + (RING - 1) * kDecodeWaves;
+          if (ALIGNED || gl < g_end)
+            load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
+                                   quarter, glane);
+          process(ring[i], gi << 4);
+        }
+      }
+      (void)VW;
+
+      // Merge the 4 waves' states in LDS: m is uniform per row, l needs the
+      // 4 lanes of a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j.
+      l_run = wave_sum16x(l_run);
+      if (quarter == 0) {
+        s_m[wave][n] = m_ref;
+        s_l[wave][n] = l_run;
+      }
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
-        const int w = j >> 1;
-        uint32_t lo, hi;
-        if ((j & 1) == 0) {
-          lo = pack_lo(r.v[0][w], r.v[1][w]);
-          hi = pack_lo(r.v[2][w], r.v[3][w]);
-        } else {
-          lo = pack_hi(r.v[0][w], r.v[1][w]);
-          hi = pack_hi(r.v[2][w], r.v[3][w]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_o[wave][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
+      }
+      __syncthreads();
+
+      for (int e = tid; e < kRows * D; e += kDecodeThreads) {
+        const int row = e / D;
+        const int d = e - row * D;
+        const int ri = rc + row;
+        if (ri >= nrows) continue;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][row]);
+        float lsum = 0.f, osum = 0.f;
+        if (mx != -INFINITY) {
+#pragma unroll
+          for (int w = 0; w < kDecodeWaves; ++w) {
+            const float sc = __builtin_amdgcn_exp2f(s_m[w][row] - mx);
+            lsum += sc * s_l[w][row];
+            osum += sc * s_o[w][row][d];
+          }
         }
-        const half4 a = __builtin_bit_cast(half4, u32x2{lo, hi});
-        acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc_o[j], 0, 0, 0);
-      }
-    };
-
-    // Groups g_begin + wave + 4k of the split, through a ring of RING register
-    // sets: RING - 1 groups are in flight while one is processed.
-    constexpr int RING = 3;
-    DecodeRegs<D> ring[RING];
-    const int g0 = g_begin + wave;
-#pragma unroll
-    for (int i = 0; i < RING - 1; ++i) {
-      const int gi = g0 + i * kDecodeWaves;
-      if (gi < g_end) load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter);
-    }
-    for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
-#pragma unroll
-      for (int i = 0; i < RING; ++i) {
-        const int gi = g + i * kDecodeWaves;
-        if (gi >= g_end) break;
-        const int gl = gi + (RING - 1) * kDecodeWaves;
-        if (gl < g_end)
-          load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
-                                 quarter);
-        process(ring[i], gi << 4);
-      }
-    }
-    (void)VW;
-
-    // Merge the 4 waves' states in LDS: m is uniform per row, l needs the
-    // 4 lanes of a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j.
-    l_run = wave_sum16x(l_run);
-    if (quarter == 0) {
-      s_m[wave][n] = m_ref;
-      s_l[wave][n] = l_run;
-    }
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_o[wave][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
-    }
-    __syncthreads();
-
-    for (int e = tid; e < kRows * D; e += kDecodeThreads) {
-      const int row = e / D;
-      const int d = e - row * D;
-      const int ri = rc + row;
-      if (ri >= nrows) continue;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][row]);
-      float lsum = 0.f, osum = 0.f;
-      if (mx != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-          const float sc = __builtin_amdgcn_exp2f(s_m[w][row] - mx);
-          lsum += sc * s_l[w][row];
-          osum += sc * s_o[w][row][d];
+        const int64_t srow = (int64_t)slot * p.dec_rows + ri;
+        p.ws_o[srow * D + d] = osum;
+        if (d == 0) {
+          p.ws_ml[srow * 2 + 0] = mx;
+          p.ws_ml[srow * 2 + 1] = lsum;
         }
       }
-      const int rhq = s_heads[ri / p.M];
-      const int rqi = ri % p.M;
-      const int64_t slot = (((int64_t)b * p.Hq + rhq) * p.M + rqi) * p.nsplit + split;
-      p.ws_o[slot * D + d] = osum;
-      if (d == 0) {
-        p.ws_ml[slot * 2 + 0] = mx;
-        p.ws_ml[slot * 2 + 1] = lsum;
-      }
+      __syncthreads();
     }
-    __syncthreads();
+
+  };
+
+  // First sequence with units at u0, then the segments of [u0, u1).
+  int lo = 0, hi = p.B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_units[mid] <= u0) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+  for (int u = u0; u < u1;) {
+    while (s_units[b + 1] <= u) ++b;
+    const int G = (s_units[b + 1] - s_units[b]) / p.Hk;
+    const int rel = u - s_units[b];
+    const int hk = rel / G;
+    const int g_lo = rel - hk * G;
+    const int uend = min(u1, s_units[b] + (hk + 1) * G);
+    segment(b, hk, g_lo, g_lo + (uend - u), b * p.Hk + hk + w);
+    u = uend;
   }
 }
 
-// Merges the split partials of one query row: one wave per (b, hq, i).
+// Merges the partials of one query row (one wave per row (b, hq, i)): the
+// workgroups whose unit range meets the row's segment are recomputed from the
+// unit prefix the decode kernel stored.
 template <int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   constexpr int DPW = D / 64;  // d values per lane
@@ -337,17 +454,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   const int b = row / (p.M * p.Hq);
   f16* op = reinterpret_cast<f16*>(p.o) + (int64_t)row * D;
 
-  const int kv_len = p.kv_len(b);
-  int kv_lim = kv_len;
-  if (p.causal) {
-    int64_t lim = (int64_t)p.q_off(b) + (p.M - 1) - p.k_off(b) + 1;
-    if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
-  }
-  const int nsp = kv_lim > 0 ? (kv_lim + p.split_tokens - 1) / p.split_tokens : 0;
-  const bool head_ok = p.kv_head(hq) >= 0;
-
+  const int hk = p.kv_head(hq);
   float result[DPW];
-  if (!head_ok) {
+  const int kv_len = p.kv_len(b);
+  if (hk < 0) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = __builtin_nanf("");
   } else if (kv_len == 0) {
@@ -356,19 +466,36 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = 0.f;
   } else {
-    const int64_t slot0 = (int64_t)row * p.nsplit;
-    float mx = -INFINITY;
-    for (int s = 0; s < nsp; ++s) mx = fmaxf(mx, p.ws_ml[(slot0 + s) * 2]);
-    float lsum = 0.f;
+    const int U = p.ws_units[p.B];
+    const int G = (p.ws_units[b + 1] - p.ws_units[b]) / p.Hk;
+    const int US = p.ws_units[b] + hk * G;
+    const int UE = US + G;
+    const int W = p.dec_wgs;
+    // Row of this query within its segment: position of hq among the heads of hk.
+    int pos = 0;
+    for (int h = 0; h < hq; ++h) pos += p.kv_head(h) == hk;
+    const int ri = pos * p.M + qi;
+    float mx = -INFINITY, lsum = 0.f;
     float acc[DPW];
 #pragma unroll
     for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
-    if (mx != -INFINITY) {
-      for (int s = 0; s < nsp; ++s) {
-        const float sc = __builtin_amdgcn_exp2f(p.ws_ml[(slot0 + s) * 2] - mx);
-        lsum += sc * p.ws_ml[(slot0 + s) * 2 + 1];
+    if (G > 0) {
+      const int wa = (int)min((int64_t)W - 1, ((int64_t)(US + 1) * W - 1) / U);
+      const int wb = (int)min((int64_t)W - 1, ((int64_t)UE * W - 1) / U);
+      for (int w = wa; w <= wb; ++w) {
+        if ((int64_t)w * U / W == (int64_t)(w + 1) * U / W) continue;  // empty range
+        const int64_t srow = (int64_t)(b * p.Hk + hk + w) * p.dec_rows + ri;
+        mx = fmaxf(mx, p.ws_ml[srow * 2]);
+      }
+      if (mx != -INFINITY) {
+        for (int w = wa; w <= wb; ++w) {
+          if ((int64_t)w * U / W == (int64_t)(w + 1) * U / W) continue;
+          const int64_t srow = (int64_t)(b * p.Hk + hk + w) * p.dec_rows + ri;
+          const float sc = __builtin_amdgcn_exp2f(p.ws_ml[srow * 2] - mx);
+          lsum += sc * p.ws_ml[srow * 2 + 1];
 #pragma unroll
-        for (int k = 0; k < DPW; ++k) acc[k] += sc * p.ws_o[(slot0 + s) * D + lane + 64 * k];
+          for (int k = 0; k < DPW; ++k) acc[k] += sc * p.ws_o[srow * D + lane + 64 * k];
+        }
       }
     }
     // No visible key (lsum == 0): 0 * inf = NaN, the reference's result for a
@@ -381,57 +508,55 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   for (int k = 0; k < DPW; ++k) op[lane + 64 * k] = (f16)result[k];
 }
 
-int env_split_tokens() {
-  static int cached = -2;
-  if (cached == -2) {
-    const char* s = getenv("FA_DECODE_SPLIT_TOKENS");
-    int v = s ? atoi(s) : 0;
-    cached = (v >= 64) ? ((v + 63) / 64) * 64 : -1;
-  }
-  return cached;
+int env_int(const char* name, int fallback) {
+  const char* s = getenv(name);
+  const int v = s ? atoi(s) : 0;
+  return v > 0 ? v : fallback;
 }
 
 }  // namespace
 
-bool use_decode_path(int M, int Hq, int Hk) {
-  if (Hk <= 0 || Hq > kMaxHeads) return false;
+bool use_decode_path(int B, int M, int Hq, int Hk) {
+  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch) return false;
   const int group = (Hq + Hk - 1) / Hk;
   return M >= 1 && (int64_t)M * group <= 4 * kRows;
 }
 
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens) {
   DecodePlan plan;
-  int split = env_split_tokens();
-  if (split < 0) split = 1024;
-  if (capacity_tokens < 1) capacity_tokens = 1;
-  plan.split_tokens = split;
-  plan.nsplit = (capacity_tokens + split - 1) / split;
-  const size_t slots = (size_t)B * Hq * M * plan.nsplit;
-  const size_t o_bytes = ((slots * D * sizeof(float)) + 255) / 256 * 256;
-  plan.ws_bytes = o_bytes + slots * 2 * sizeof(float);
-  (void)Hk;
+  // Enough workgroups to fill every CU several times over, but not more than
+  // the largest possible number of 16-key groups divided by 8.
+  const int64_t max_units = (int64_t)B * Hk * ((capacity_tokens + 15) / 16);
+  int64_t wgs = env_int("FA_DECODE_WGS", 1024);
+  wgs = std::min<int64_t>(wgs, std::max<int64_t>(1, max_units / 8));
+  plan.wgs = (int)wgs;
+  plan.rows = Hq * M;
+  const size_t slots = (size_t)B * Hk + (size_t)plan.wgs;
+  plan.o_bytes = (slots * plan.rows * D * sizeof(float) + 255) / 256 * 256;
+  plan.ml_bytes = (slots * plan.rows * 2 * sizeof(float) + 255) / 256 * 256;
+  plan.ws_bytes = plan.o_bytes + plan.ml_bytes + (size_t)(B + 1) * sizeof(int);
   return plan;
 }
 
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
-  const dim3 grid((unsigned)p.nsplit, (unsigned)p.Hk, (unsigned)p.B);
+  const dim3 grid((unsigned)p.dec_wgs);
   const int rows = p.B * p.Hq * p.M;
   const dim3 cgrid((unsigned)((rows + 3) / 4));
   const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
   const dim3 block(kDecodeThreads);
   if (D == 128) {
     if (aligned)
-      hipLaunchKernelGGL((decode_split_kernel<128, true>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_split_kernel<128, false>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
   } else {
     if (aligned)
-      hipLaunchKernelGGL((decode_split_kernel<64, true>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((decode_split_kernel<64, false>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(256), 0, stream, p);

@@ -79,11 +79,15 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
 
 def test_workspace_sizing_depends_on_sizes_only():
     lib = _lib.load()
-    # decode (M = 1): (D + 2) floats per (b, hq, split), 256-byte aligned o part
+    # decode (M = 1): partial slots (B*Hk + workgroups) x (Hq*M rows) x (D + 2)
+    # floats (two 256-byte aligned parts) + the (B + 1) unit prefix; 1024
+    # workgroups unless a batch has fewer than 8 groups of 16 keys per workgroup.
     ws = lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16)
-    nsplit = -(-1025 * 16 // 1024)
-    o_bytes = -(-(64 * 64 * nsplit * 128 * 4) // 256) * 256
-    assert ws == o_bytes + 64 * 64 * nsplit * 2 * 4
+    slots = 64 * 8 + 1024
+    align = lambda x: -(-x // 256) * 256  # noqa: E731
+    assert ws == align(slots * 64 * 128 * 4) + align(slots * 64 * 2 * 4) + 65 * 4
+    small = lib.fa_paged_workspace_bytes(1, 8, 1, 64, 8, 2, 16)  # 16 units -> 2 workgroups
+    assert small == align((8 + 2) * 8 * 64 * 4) + align((8 + 2) * 8 * 2 * 4) + 2 * 4
     # prefill-shaped calls need no workspace
     assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16) == 0
     assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16) == 0
