@@ -18,7 +18,7 @@ Per-kernel durations come from HIP events recorded on the stream the kernels
 run on (torch's current stream) around every timed launch; `roofline.achieved`
 is algorithmic work per launch / mean launch duration. The CPU baseline is the
 oracle's restatement of the reference's CPU math path
-(flashattention_custom/ops.py:37-75), timed on the host (kind "port").
+(flashattention_custom/ops.py:34-72), timed on the host (kind "port").
 """
 from __future__ import annotations
 

@@ -2,7 +2,7 @@
 //
 // Semantics follow the reference's paged_kv_append_kernel
 // (csrc/flash_attn_sm75.cu:528-555) and its CPU twin
-// (flashattention_custom/ops.py:66-75): token t of sequence b goes to position
+// (flashattention_custom/ops.py:63-72): token t of sequence b goes to position
 // start + t, i.e. page (start+t)/PS, slot (start+t)%PS, for every KV head.
 // Positions whose page is out of range are skipped (reference :548).
 //

@@ -4,7 +4,7 @@
 // causal=False; engine/llama_tp.py:186-200), i.e. for query row (b, hq, i)
 //   o = softmax_j(q . k_j / sqrt(D)) v_j over keys j < seqlen[b]
 // (and k_off + j <= q_off + i when causal), with K/V of head head_map[hq]
-// (flashattention_custom/ops.py:37-63, csrc/flash_attn_sm75.cu:213-425).
+// (flashattention_custom/ops.py:34-60, csrc/flash_attn_sm75.cu:213-425).
 //
 // Design (HBM-bound; every K/V byte is read once per KV head):
 //  * The work is split evenly: the (sequence, KV head, 16-token group) units
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     for (int k = 0; k < DPW; ++k) result[k] = __builtin_nanf("");
   } else if (kv_len == 0) {
     // Zero keys: softmax over an empty row times an empty V is zero
-    // (flashattention_custom/ops.py:55-62 with slen == 0).
+    // (flashattention_custom/ops.py:39, 52-59 with slen == 0).
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = 0.f;
   } else {

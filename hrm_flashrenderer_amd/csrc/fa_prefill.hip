@@ -2,7 +2,7 @@
 // K/V, MHA or GQA), and an fp32 variant of the contiguous op.
 //
 // Semantics: the reference's flash_attn / flash_attn_paged
-// (flashattention_custom/ops.py:22-63, csrc/flash_attn_sm75.cu:89-425):
+// (flashattention_custom/ops.py:19-60, csrc/flash_attn_sm75.cu:89-425):
 //   O[b,h,i] = sum_j softmax_j(Q[b,h,i] . K[b,hk,j] / sqrt(D)) V[b,hk,j]
 // over keys j < N_b with k_off + j <= q_off + i when causal.
 //
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_dma_kernel(AttnParams p, 
 }
 
 // fp32 contiguous attention (the reference's CPU path accepts fp32,
-// flashattention_custom/ops.py:22-34). Exact fp32 arithmetic on the vector
+// flashattention_custom/ops.py:19-31). Exact fp32 arithmetic on the vector
 // ALUs: one wave of 64 query rows per workgroup, Q rows in LDS, K/V streamed
 // in 16-key tiles.
 template <int D>

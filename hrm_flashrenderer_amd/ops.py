@@ -202,7 +202,7 @@ def validate_flash_attn(q, k, v, require_device: bool = True) -> None:
 def flash_attn(q, k, v, causal=True, q_offset=0, k_offset=0):
     """Contiguous attention O = softmax(Q K^T / sqrt(D), causal mask) V.
 
-    Reference: flashattention_custom/ops.py:82-85 -> csrc/ext.cpp:30-40.
+    Reference: flashattention_custom/ops.py:79-82 -> csrc/ext.cpp:30-40.
     q [B,Hq,M,D], k/v [B,Hk,N,D]; returns a new tensor shaped like q.
     """
     validate_flash_attn(q, k, v)
@@ -246,7 +246,7 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
                      causal=True, q_offset=0, k_offset=0, *, block_table=None):
     """Attention of q over paged K/V (prefill chunk or decode).
 
-    Reference: flashattention_custom/ops.py:88-95 -> csrc/ext.cpp:42-68.
+    Reference: flashattention_custom/ops.py:85-92 -> csrc/ext.cpp:42-68.
     q [B,Hq,M,D] fp16; k_pages/v_pages [NB,Hk,P,PS,D] fp16; seqlen int32 [B];
     head_map int32 [Hq]. Returns a new tensor shaped like q.
     """
@@ -294,7 +294,7 @@ def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_siz
 def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, block_table=None):
     """Write k_new/v_new [B,Hk,T,D] at positions start_pos + t of each sequence, in place.
 
-    Reference: flashattention_custom/ops.py:98-102 -> csrc/ext.cpp:70-89.
+    Reference: flashattention_custom/ops.py:95-99 -> csrc/ext.cpp:70-89.
     A Python-int start_pos is range-checked against the page capacity and
     raises; per-sequence (tensor) starts skip out-of-range positions on the
     device, as the reference kernel does (csrc/flash_attn_sm75.cu:548).

@@ -15,7 +15,7 @@
  *   - Return value: 0 on success, a negative FA_ERR_* code otherwise; the
  *     message of the last failure on the calling thread is fa_last_error().
  *
- * Paged K/V layout (reference: csrc/flash_attn_sm75.cu:54-86, ops.py:37-48)
+ * Paged K/V layout (reference: csrc/flash_attn_sm75.cu:54-86, ops.py:34-45)
  *   k_pages, v_pages : fp16 [NB, Hk, P, PS, D]
  *   Token `pos` of sequence b lives in logical page pos / PS, slot pos % PS.
  *   Logical page p of sequence b maps to a physical page id phi:
@@ -60,7 +60,7 @@ extern "C" {
  *   k_off + j <= q_off + i, where q_off = q_offsets ? q_offsets[b] : q_offset
  *   (likewise k_off). q_offsets / k_offsets are nullable int32 [B] buffers.
  *   A row with no visible key (N > 0) yields NaN, and N == 0 yields zeros, as
- *   in the reference's CPU math (flashattention_custom/ops.py:22-34).
+ *   in the reference's CPU math (flashattention_custom/ops.py:19-31).
  */
 int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
                       int dtype, int B, int Hq, int Hk, int M, int N, int D,

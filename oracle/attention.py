@@ -13,19 +13,19 @@ Contents
        gather_kv                pages -> contiguous [B, Hk, cap, D]
        append_f16               closed-form index map of paged_kv_append
   3. Restatement of the reference's CPU math path (torch, same operation
-     sequence and dtypes as flashattention_custom/ops.py:22-75), the "port"
+     sequence and dtypes as flashattention_custom/ops.py:19-72), the "port"
      timed as the CPU baseline; pinned bit-for-bit by the golden vectors in
      tests/golden/ that the reference itself produced.
-       cpu_flash_attn           ops.py:22-34
-       cpu_flash_attn_paged     ops.py:37-63 (+ block table / per-seq offsets)
-       cpu_paged_kv_append      ops.py:66-75 (+ block table / per-seq starts)
+       cpu_flash_attn           ops.py:19-31
+       cpu_flash_attn_paged     ops.py:34-60 (+ block table / per-seq offsets)
+       cpu_paged_kv_append      ops.py:63-72 (+ block table / per-seq starts)
 
 How each function is pinned (tests/test_oracle.py):
   attention_f64     brute-force triple loop on tiny shapes; torch SDPA in
                     float64 with an explicit mask; invariants (one visible key
                     -> v, equal scores -> mean of V, shift invariance, key
                     permutation invariance, GQA == MHA with repeated K/V).
-  gather_kv         identity block table == reference flatten (ops.py:43-48);
+  gather_kv         identity block table == reference flatten (ops.py:43-45);
                     a permuted pool gathered == the unpermuted original.
   append_f16        the reference's append known-answer test shape
                     (flash_tests/test_append_fast.py:16-38) against an
@@ -67,7 +67,7 @@ def attention_f64(q: ArrayLike, k: ArrayLike, v: ArrayLike, causal: bool = True,
     q [B,Hq,M,D]; k, v [B,Hk,N,D] (contiguous view of the keys of each
     sequence). Key j is visible to row i of sequence b iff j < kv_len[b] and,
     when causal, k_off[b] + j <= q_off[b] + i (reference semantics:
-    flash_attn_sm75.cu:65-71, :164, :328; ops.py:28-32, :56-60). q head h reads
+    flash_attn_sm75.cu:65-71, :164, :328; ops.py:25-29, :53-57). q head h reads
     K/V head head_map[h] (default h // (Hq // Hk)).
     A row with no visible key is NaN when kv_len > 0 and 0 when kv_len == 0
     (empty softmax times empty V), matching ops.py.
@@ -139,7 +139,7 @@ def gather_kv(pages: ArrayLike, B: int, page_size: int,
               block_table: Optional[ArrayLike] = None) -> np.ndarray:
     """Gather a paged pool [NB,Hk,P,PS,D] into contiguous [B,Hk,cap,D].
 
-    cap = P*PS without a block table (the reference flatten of ops.py:43-48),
+    cap = P*PS without a block table (the reference flatten of ops.py:43-45),
     else max_blocks*PS; logical page p of sequence b is pool page
     phi = block_table[b, p] -> pages[phi // P, :, phi % P]. Unmapped pages
     (phi < 0) read as NaN so that any use of them is visible.
@@ -164,7 +164,7 @@ def append_f16(k_pages: ArrayLike, v_pages: ArrayLike, k_new: ArrayLike, v_new: 
     """Closed-form result of paged_kv_append (returns new numpy arrays).
 
     pos = start_b + t goes to logical page pos // PS, slot pos % PS
-    (flash_attn_sm75.cu:545-554, ops.py:66-75); positions whose page is
+    (flash_attn_sm75.cu:545-554, ops.py:63-72); positions whose page is
     negative, beyond the capacity, or unmapped are skipped (:548).
     """
     kp = _np(k_pages).copy()
@@ -207,7 +207,7 @@ def _mask_scores(scores: torch.Tensor, causal: bool, q_off: int, k_off: int) -> 
 
 def cpu_flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
                    q_offset: int = 0, k_offset: int = 0) -> torch.Tensor:
-    """ops.py:22-34: fp32 scores and softmax, P cast to q.dtype, batched P @ V."""
+    """ops.py:19-31: fp32 scores and softmax, P cast to q.dtype, batched P @ V."""
     inv_sqrt_d = 1.0 / math.sqrt(q.shape[-1])
     scores = torch.matmul(q.float(), k.float().transpose(-1, -2)) * inv_sqrt_d
     scores = _mask_scores(scores, causal, int(q_offset), int(k_offset))
@@ -221,7 +221,7 @@ def cpu_flash_attn_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
                          block_table: Optional[torch.Tensor] = None,
                          batches: Optional[Sequence[int]] = None,
                          heads: Optional[Sequence[int]] = None) -> torch.Tensor:
-    """ops.py:37-63: per sequence, flatten its first ceil(slen/PS) pages, then
+    """ops.py:34-60: per sequence, flatten its first ceil(slen/PS) pages, then
     per query head a 2-D fp32 score matmul, fp32 softmax cast to q.dtype, and
     P @ V in q.dtype, written into a zero-initialised output.
 
@@ -262,7 +262,7 @@ def cpu_flash_attn_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
 def cpu_paged_kv_append(k_pages: torch.Tensor, v_pages: torch.Tensor, k_new: torch.Tensor,
                         v_new: torch.Tensor, start_pos, page_size: int,
                         block_table: Optional[torch.Tensor] = None) -> None:
-    """ops.py:66-75: per sequence and token, copy the [Hk, D] slice into its slot (in place)."""
+    """ops.py:63-72: per sequence and token, copy the [Hk, D] slice into its slot (in place)."""
     B, Hk, T, D = k_new.shape
     P = k_pages.shape[2]
     starts = _per_seq(start_pos, B)

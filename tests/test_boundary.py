@@ -4,7 +4,7 @@
 * The C ABI rejects bad arguments with status codes and the reference's
   messages before touching the device.
 * The Python API keeps the reference's names, positional order and defaults
-  (flashattention_custom/ops.py:82-102) and raises the reference extension's
+  (flashattention_custom/ops.py:79-99) and raises the reference extension's
   messages (csrc/ext.cpp:31-87) for bad arguments.
 * The custom ops are registered with shape-only (fake) implementations.
 """
@@ -94,7 +94,7 @@ def test_workspace_sizing_depends_on_sizes_only():
 
 
 def test_signatures_match_reference():
-    # flashattention_custom/ops.py:82, 88-89, 98
+    # flashattention_custom/ops.py:81, 88-90, 97
     def params(fn):
         return [(p.name, p.default) for p in inspect.signature(fn).parameters.values()
                 if p.kind is not inspect.Parameter.KEYWORD_ONLY]
