@@ -221,9 +221,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   __shared__ int s_count;
   __shared__ int s_units[kMaxBatch + 1];
   __shared__ int s_part[kDecodeThreads];
-  __shared__ float s_m[kDecodeWaves][kRows];
-  __shared__ float s_l[kDecodeWaves][kRows];
-  __shared__ float s_o[kDecodeWaves][kRows][OPAD];
+  // Wave merge buffers: waves 2 and 3 hand their state to waves 0 and 1, which
+  // then publish the pairwise merge (half the LDS of one slot per wave, so four
+  // workgroups fit on a CU).
+  __shared__ float s_m[2][kRows];
+  __shared__ float s_l[2][kRows];
+  __shared__ float s_o[2][kRows][OPAD];
 
   const int w = blockIdx.x;
   const int W = gridDim.x;
@@ -382,17 +385,44 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       }
       (void)VW;
 
-      // Merge the 4 waves' states in LDS: m is uniform per row, l needs the
-      // 4 lanes of a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j.
+      // Merge the 4 waves' states: m is uniform per row, l needs the 4 lanes of
+      // a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j. Waves 2, 3
+      // pass their state to waves 0, 1 (in registers there), which publish the
+      // pair merge; the workgroup then merges the two pairs per element.
       l_run = wave_sum16x(l_run);
-      if (quarter == 0) {
-        s_m[wave][n] = m_ref;
-        s_l[wave][n] = l_run;
+      const int half = wave & 1;
+      if (wave >= 2) {
+        if (quarter == 0) {
+          s_m[half][n] = m_ref;
+          s_l[half][n] = l_run;
+        }
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s_o[half][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
+        }
       }
+      __syncthreads();
+      if (wave < 2) {
+        const float m_o = s_m[half][n];
+        const float mx = fmaxf(m_ref, m_o);
+        const float a = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - mx);
+        const float bsc = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_o - mx);
+        l_run = l_run * a + s_l[half][n] * bsc;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
+        for (int j = 0; j < DPL; ++j) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s_o[wave][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
+          for (int r = 0; r < 4; ++r) {
+            float& x = s_o[half][n][DPL * (4 * quarter + r) + j];
+            x = acc_o[j][r] * a + x * bsc;
+          }
+        }
+        // all lanes of the row have read s_m / s_l before they are replaced
+        __builtin_amdgcn_wave_barrier();
+        if (quarter == 0) {
+          s_m[half][n] = mx;
+          s_l[half][n] = l_run;
+        }
       }
       __syncthreads();
 
@@ -401,19 +431,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         const int d = e - row * D;
         const int ri = rc + row;
         if (ri >= nrows) continue;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_m[w][row]);
+        const float m0 = s_m[0][row], m1 = s_m[1][row];
+        const float mx = fmaxf(m0, m1);
         float lsum = 0.f, osum = 0.f;
         if (mx != -INFINITY) {
-#pragma unroll
-          for (int w = 0; w < kDecodeWaves; ++w) {
-            const float sc = __builtin_amdgcn_exp2f(s_m[w][row] - mx);
-            lsum += sc * s_l[w][row];
-            osum += sc * s_o[w][row][d];
-          }
+          const float a0 = __builtin_amdgcn_exp2f(m0 - mx);
+          const float a1 = __builtin_amdgcn_exp2f(m1 - mx);
+          lsum = a0 * s_l[0][row] + a1 * s_l[1][row];
+          osum = a0 * s_o[0][row][d] + a1 * s_o[1][row][d];
         }
-        const int64_t srow = (int64_t)slot * p.dec_rows + ri;
+        // partial rows are indexed by (q head, query position) of the sequence
+        const int hrow = s_heads[ri / p.M] * p.M + ri % p.M;
+        const int64_t srow = (int64_t)slot * p.dec_rows + hrow;
         p.ws_o[srow * D + d] = osum;
         if (d == 0) {
           p.ws_ml[srow * 2 + 0] = mx;
@@ -476,10 +505,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     const int US = p.ws_units[b] + hk * G;
     const int UE = US + G;
     const int W = p.dec_wgs;
-    // Row of this query within its segment: position of hq among the heads of hk.
-    int pos = 0;
-    for (int h = 0; h < hq; ++h) pos += p.kv_head(h) == hk;
-    const int ri = pos * p.M + qi;
+    const int64_t rbase = (int64_t)(b * p.Hk + hk) * p.dec_rows + (int64_t)hq * p.M + qi;
     float mx = -INFINITY, lsum = 0.f;
     float acc[DPW];
 #pragma unroll
@@ -487,20 +513,37 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     if (G > 0) {
       const int wa = (int)min((int64_t)W - 1, ((int64_t)(US + 1) * W - 1) / U);
       const int wb = (int)min((int64_t)W - 1, ((int64_t)UE * W - 1) / U);
-      for (int w = wa; w <= wb; ++w) {
-        if ((int64_t)w * U / W == (int64_t)(w + 1) * U / W) continue;  // empty range
-        const int64_t srow = (int64_t)(b * p.Hk + hk + w) * p.dec_rows + ri;
-        mx = fmaxf(mx, p.ws_ml[srow * 2]);
-      }
-      if (mx != -INFINITY) {
-        for (int w = wa; w <= wb; ++w) {
-          if ((int64_t)w * U / W == (int64_t)(w + 1) * U / W) continue;
-          const int64_t srow = (int64_t)(b * p.Hk + hk + w) * p.dec_rows + ri;
-          const float sc = __builtin_amdgcn_exp2f(p.ws_ml[srow * 2] - mx);
-          lsum += sc * p.ws_ml[srow * 2 + 1];
+      // Slots in batches of 4 with every load issued before the merge; slots
+      // of workgroups with an empty unit range were never written.
+      constexpr int kBatch = 4;
+      for (int w0 = wa; w0 <= wb; w0 += kBatch) {
+        float pm[kBatch], pl[kBatch], po[kBatch][DPW];
 #pragma unroll
-          for (int k = 0; k < DPW; ++k) acc[k] += sc * p.ws_o[srow * D + lane + 64 * k];
+        for (int i = 0; i < kBatch; ++i) {
+          const int w = w0 + i;
+          const bool live = w <= wb && (int64_t)w * U / W != (int64_t)(w + 1) * U / W;
+          const int64_t srow = rbase + (int64_t)w * p.dec_rows;
+          pm[i] = live ? p.ws_ml[srow * 2] : -INFINITY;
+          pl[i] = live ? p.ws_ml[srow * 2 + 1] : 0.f;
+#pragma unroll
+          for (int k = 0; k < DPW; ++k) po[i][k] = live ? p.ws_o[srow * D + lane + 64 * k] : 0.f;
         }
+        float bm = mx;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) bm = fmaxf(bm, pm[i]);
+        if (bm == -INFINITY) continue;
+        const float r = __builtin_amdgcn_exp2f(mx - bm);  // mx == -inf gives 0
+        lsum *= r;
+#pragma unroll
+        for (int k = 0; k < DPW; ++k) acc[k] *= r;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const float sc = __builtin_amdgcn_exp2f(pm[i] - bm);
+          lsum += sc * pl[i];
+#pragma unroll
+          for (int k = 0; k < DPW; ++k) acc[k] += sc * po[i][k];
+        }
+        mx = bm;
       }
     }
     // No visible key (lsum == 0): 0 * inf = NaN, the reference's result for a
