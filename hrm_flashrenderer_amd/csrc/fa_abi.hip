@@ -193,7 +193,7 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
     p.ws_o = reinterpret_cast<float*>(ws);
     p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
     p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-    p.dec_wgs = plan.wgs;
+    p.dec_wgs = fa::decode_launch_wgs(plan, D, PS % 16 == 0);
     p.dec_rows = plan.rows;
     return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
   }

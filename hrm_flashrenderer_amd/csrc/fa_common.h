@@ -129,13 +129,15 @@ hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
 
 // Decode sizing (host side; depends on sizes only).
 struct DecodePlan {
-  int wgs;          // workgroups sharing the work evenly
+  int wgs;          // workgroup capacity of the workspace
   int rows;         // row capacity of a partial slot
   size_t o_bytes;   // partial O, 256-byte aligned
   size_t ml_bytes;  // partial (max, sum), 256-byte aligned
   size_t ws_bytes;  // total, including the unit prefix
 };
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
+// Workgroups to launch for a plan on the current device (<= plan.wgs).
+int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned);
 bool use_decode_path(int B, int M, int Hq, int Hk);
 
 }  // namespace fa

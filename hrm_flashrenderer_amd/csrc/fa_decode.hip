@@ -36,6 +36,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 namespace fa {
 
@@ -570,10 +571,46 @@ bool use_decode_path(int B, int M, int Hq, int Hk) {
   return M >= 1 && (int64_t)M * group <= 4 * kRows;
 }
 
+int resident_decode_wgs(int D, bool aligned) {
+  // Workgroups of the decode kernel that are resident at once on the current
+  // device (CUs x workgroups per CU), cached per device and kernel variant.
+  // Launching exactly this many gives every workgroup its equal share in a
+  // single round; a partial second round leaves CUs idle.
+  static std::atomic<int> cache[64][4];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int idx = (D == 128 ? 2 : 0) + (aligned ? 1 : 0);
+  int v = cache[dev][idx].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per_cu = 0;
+  const void* fn = nullptr;
+  if (D == 128)
+    fn = aligned ? reinterpret_cast<const void*>(&decode_kernel<128, true>)
+                 : reinterpret_cast<const void*>(&decode_kernel<128, false>);
+  else
+    fn = aligned ? reinterpret_cast<const void*>(&decode_kernel<64, true>)
+                 : reinterpret_cast<const void*>(&decode_kernel<64, false>);
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDecodeThreads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  v = cus * per_cu;
+  if (v > 0) cache[dev][idx].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned) {
+  if (getenv("FA_DECODE_WGS") != nullptr) return plan.wgs;
+  const int r = resident_decode_wgs(D, aligned);
+  return r > 0 ? std::min(plan.wgs, r) : plan.wgs;
+}
+
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens) {
   DecodePlan plan;
-  // Enough workgroups to fill every CU several times over, but not more than
-  // the largest possible number of 16-key groups divided by 8.
+  // Workspace capacity: up to 1024 workgroups (FA_DECODE_WGS overrides), but
+  // not more than the largest possible number of 16-key groups divided by 8.
+  // The launch uses min(this, the device's resident workgroups).
   const int64_t max_units = (int64_t)B * Hk * ((capacity_tokens + 15) / 16);
   int64_t wgs = env_int("FA_DECODE_WGS", 1024);
   wgs = std::min<int64_t>(wgs, std::max<int64_t>(1, max_units / 8));
