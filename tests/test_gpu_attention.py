@@ -111,13 +111,13 @@ def test_contiguous_gqa_offsets_noncausal(gpu, dtype, D):
 # ----------------------------------------------------------- paged path ----
 
 def _small_paged(B, Hq, Hk, M, lengths, PS=16, D=128, seed=0, causal=True, q_offsets=None,
-                 spare_pages=5):
+                 spare_pages=5, max_blocks=None):
     dev = torch.device("cuda", 0)
     g = torch.Generator().manual_seed(seed)
     pages = [(n + PS - 1) // PS for n in lengths]
     total = sum(pages) + spare_pages
     perm = torch.randperm(total, generator=g).to(torch.int32)
-    max_blocks = max(pages) + 2
+    max_blocks = max(pages) + 2 if max_blocks is None else max_blocks
     bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
     pos = 0
     for b, n in enumerate(pages):
@@ -149,6 +149,34 @@ def _run_and_check(c, what, rows=None):
 def test_paged_prefill_gqa_block_table(gpu, D):
     c = _small_paged(2, 10, 2, 300, [300, 300], D=D, seed=10 + D)
     _run_and_check(c, "prefill")
+
+
+@pytest.mark.parametrize("capacity_blocks", [None, 300])
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_tile_kernels_short_and_long_capacity(gpu, D, capacity_blocks):
+    """The same inputs through both DMA prefill kernels: a block table of at most
+    4096 keys of capacity selects the 32-key-tile kernel, a wider one (300 pages
+    of 16 = 4800 keys) the pipelined 64-key-tile kernel."""
+    prior = [0, 133, 0, 61]
+    M = 200
+    lengths = [p + M for p in prior]
+    c = _small_paged(4, 8, 2, M, lengths, D=D, seed=40 + D, q_offsets=prior,
+                     max_blocks=capacity_blocks)
+    _run_and_check(c, f"causal cap={capacity_blocks}")
+    c = _small_paged(3, 8, 2, 70, [200, 333, 97], D=D, seed=50 + D, causal=False,
+                     max_blocks=capacity_blocks)
+    _run_and_check(c, f"non-causal cap={capacity_blocks}")
+
+
+def test_contiguous_long_rows(gpu):
+    """Contiguous K/V longer than 4096 keys (the pipelined kernel), causal with an
+    offset and non-causal, N not a multiple of the tile."""
+    B, Hq, Hk, M, N, D = 1, 4, 2, 96, 4203, 128
+    q, k, v = seeded((B, Hq, M, D), 60), seeded((B, Hk, N, D), 61), seeded((B, Hk, N, D), 62)
+    for causal, qo in ((True, N - M), (False, 0), (True, 2000)):
+        out = flash_attn(q, k, v, causal, qo, 0).cpu()
+        assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal, qo, 0),
+                     f"long rows causal={causal} qo={qo}")
 
 
 def test_chunked_prefill_per_sequence_offsets(gpu):
