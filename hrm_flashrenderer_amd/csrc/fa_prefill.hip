@@ -346,6 +346,16 @@ constexpr float kRescaleLog2 = 8.f;
 
 __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
+// Max of 16 values as a depth-3 tree of max3 (six independent max3, then two,
+// then one), instead of a dependent chain of eight.
+__device__ __forceinline__ float max16(const floatx16& s) {
+  const float a0 = max3f(s[0], s[1], s[2]), a1 = max3f(s[3], s[4], s[5]);
+  const float a2 = max3f(s[6], s[7], s[8]), a3 = max3f(s[9], s[10], s[11]);
+  const float a4 = max3f(s[12], s[13], s[14]);
+  const float b0 = max3f(a0, a1, a2), b1 = max3f(a3, a4, s[15]);
+  return fmaxf(b0, b1);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            (int)kRsrcWord3);
@@ -403,7 +413,7 @@ template <int D, int NW, int BN = kBN>
 __device__ __forceinline__ QuarterSrc slab_src(const AttnParams& p, int b, int hk, int k0,
                                                int kv_len, int wave) {
   using C = DmaCfg<D>;
-  constexpr int SLAB = Slab<D, NW, BN>::SLAB;
+  constexpr int SLAB = BN / NW;
   const int g0 = k0 + SLAB * wave;
   const int valid = min(SLAB, kv_len - g0);
   QuarterSrc q{0, 0u};
@@ -413,6 +423,45 @@ __device__ __forceinline__ QuarterSrc slab_src(const AttnParams& p, int b, int h
   }
   return q;
 }
+
+// Per-wave page table in VGPR lanes: lane i holds the key-row index (element
+// offset / D) of this wave's slab of tiles base + i and base + 64 + i, or ~0u
+// when the slab has no addressable row. One vector pass (block-table loads
+// included) covers 128 tiles; a tile's lookup is then one v_readlane, so the
+// tile loop issues no scalar loads (whose lgkmcnt wait would also drain the
+// LDS reads in flight). Row indices fit 32 bits: 2^32 rows of >= 128 bytes
+// exceed the device memory.
+template <int D, int NW, int BN = kBN>
+struct SlabTable {
+  static constexpr int SPAN = 128;
+  uint32_t lo, hi;
+  int base;
+
+  __device__ static uint32_t row(const AttnParams& p, int b, int hk, int T, int kv_len, int wave) {
+    const int g0 = T * BN + (BN / NW) * wave;
+    if (g0 < 0 || g0 >= kv_len) return ~0u;
+    const int64_t off = p.kv.row_offset(b, hk, g0);
+    return off < 0 ? ~0u : (uint32_t)(off / D);
+  }
+  __device__ void fill(const AttnParams& p, int b, int hk, int kv_len, int wave, int lane, int first) {
+    base = first;
+    lo = row(p, b, hk, first + lane, kv_len, wave);
+    hi = row(p, b, hk, first + 64 + lane, kv_len, wave);
+  }
+  // Source of tile T (uniform) for this wave.
+  __device__ QuarterSrc get(const AttnParams& p, int b, int hk, int T, int kv_len, int wave,
+                            int lane) {
+    if (T >= base + SPAN) fill(p, b, hk, kv_len, wave, lane, T);
+    const int i = T - base;
+    const uint32_t r = i < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)lo, i)
+                              : (uint32_t)__builtin_amdgcn_readlane((int)hi, i - 64);
+    const int g0 = T * BN + (BN / NW) * wave;
+    const int valid = min(BN / NW, kv_len - g0);
+    QuarterSrc q{0, 0u};
+    if (r != ~0u && valid > 0) q = QuarterSrc{(int64_t)r * D, (uint32_t)(valid * DmaCfg<D>::ROWB)};
+    return q;
+  }
+};
 
 template <int D, int NW, int BN = kBN>
 struct SlabLane {
@@ -468,12 +517,7 @@ __device__ __forceinline__ void mask_tile(floatx16& s0, floatx16& s1, int k0, in
 }
 
 __device__ __forceinline__ float tile_max(const floatx16& s0, const floatx16& s1) {
-  float mx = max3f(s0[0], s0[1], s0[2]);
-#pragma unroll
-  for (int r = 3; r < 15; r += 2) mx = max3f(mx, s0[r], s0[r + 1]);
-#pragma unroll
-  for (int r = 0; r < 16; r += 2) mx = max3f(mx, s1[r], s1[r + 1]);
-  return fmaxf(mx, s0[15]);
+  return fmaxf(max16(s0), max16(s1));
 }
 
 template <int D>
@@ -649,7 +693,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_pipe_kernel(AttnParams p,
     // 32..63 (n1) during the second half, so at most three 16-register S
     // blocks are live at a time.
     half8 pb[4];
-    float psum = 0.f;
+    float ps[2] = {0.f, 0.f};  // two independent row-sum chains
     const char* kb = kbuf0 + (PB ^ 1) * C::TILE;
     auto half_block = [&](floatx16& nacc, const floatx16& cur, int kbase, int pbase) {
       half8 ka[KA];
@@ -671,14 +715,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_pipe_kernel(AttnParams p,
           const f16 e1 = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(cur[idx + 1], c, -m_use));
           pb[pbase + (idx >> 3)][idx & 7] = e0;
           pb[pbase + (idx >> 3)][(idx & 7) + 1] = e1;
-          psum = __builtin_amdgcn_fdot2(half2v{e0, e1}, ones, psum, false);
+          ps[ks & 1] = __builtin_amdgcn_fdot2(half2v{e0, e1}, ones, ps[ks & 1], false);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     };
     half_block(n0, c0, 0, 0);
     half_block(n1, c1, 32 * C::ROWB, 2);
-    l_run += psum;
+    l_run += ps[0] + ps[1];
 
     // O^T += V_t^T P_t^T: operands read VA MFMAs ahead.
     const char* vb = vbuf0 + PB * C::TILE;
@@ -787,12 +831,14 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const char* kp = reinterpret_cast<const char*>(p.k);
   const char* vp = reinterpret_cast<const char*>(p.v);
   const SlabLane<D, NW, BN> dl = slab_lane<D, NW, BN>(wave, lane);
+  SlabTable<D, NW, BN> pages;
+  pages.fill(p, b, hk, kv_len, wave, lane, 0);
   if (ntiles > 0) {
-    const QuarterSrc s0 = slab_src<D, NW, BN>(p, b, hk, 0, kv_len, wave);
+    const QuarterSrc s0 = pages.get(p, b, hk, 0, kv_len, wave, lane);
     dma_slab<D, NW, BN>(s0, dl.vk, kp, wave, smem);
     dma_slab<D, NW, BN>(s0, dl.vv, vp, wave, smem + TILE);
   }
-  QuarterSrc next_src = slab_src<D, NW, BN>(p, b, hk, BN, kv_len, wave);
+  QuarterSrc next_src = pages.get(p, b, hk, 1, kv_len, wave, lane);
 
   const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
   half8 qreg[KSTEPS];
@@ -803,17 +849,18 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
                    : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  int koff[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks)
-    koff[ks] = col * C::ROWB + 16 * ((2 * ks + half_id) ^ C::swz_k(col));
+  // LDS byte offsets of the lane's operands. K: row col, logical chunk
+  // 2*ks + half_id at chunk ^ swz_k(col); the chunk bits of 2*ks and half_id
+  // are disjoint, so the k-step ks offset is kbase ^ (32 * ks). V (transposing
+  // read, d = 32*i + 16*(gq%2) + 4*(sl%4)): likewise vbase ^ (64 * i). Both
+  // are recomputed per tile (one XOR per read) rather than held in registers.
   const int gq = lane >> 4, sl = lane & 15;
   const int vrow = 4 * (gq >> 1) + (sl >> 2);
-  int voff[DBLK];
-#pragma unroll
-  for (int i = 0; i < DBLK; ++i) {
-    const int d = 32 * i + 16 * (gq & 1) + 4 * (sl & 3);
-    voff[i] = TILE + vrow * C::ROWB + 16 * ((d >> 3) ^ C::swz_v(vrow)) + 2 * (d & 7);
+  int kbase = col * C::ROWB + 16 * (half_id ^ C::swz_k(col));
+  int vbase;
+  {
+    const int d = 16 * (gq & 1) + 4 * (sl & 3);
+    vbase = TILE + vrow * C::ROWB + 16 * ((d >> 3) ^ C::swz_v(vrow)) + 2 * (d & 7);
   }
 
   floatx16 acc_o[DBLK];
@@ -833,10 +880,16 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       char* nbuf = smem + (PB ^ 1) * 2 * TILE;
       dma_slab<D, NW, BN>(next_src, dl.vk, kp, wave, nbuf);
       dma_slab<D, NW, BN>(next_src, dl.vv, vp, wave, nbuf + TILE);
-      next_src = slab_src<D, NW, BN>(p, b, hk, k0 + 2 * BN, kv_len, wave);
+      if (t + 2 < ntiles) next_src = pages.get(p, b, hk, t + 2, kv_len, wave, lane);
     }
     if (k0 >= wave_lim_max) return;
     const char* buf = smem + PB * 2 * TILE;
+    asm volatile("" : "+v"(kbase), "+v"(vbase));  // keep the XORs below in the loop
+    int koff[KSTEPS], voff[DBLK];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) koff[ks] = kbase ^ (32 * ks);
+#pragma unroll
+    for (int i = 0; i < DBLK; ++i) voff[i] = vbase ^ (64 * i);
 
     constexpr int KA = 2;
     floatx16 s0 = floatx16{};
@@ -861,10 +914,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
         if (key >= lim) s0[r] = -INFINITY;
       }
     }
-    float mx = max3f(s0[0], s0[1], s0[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = max3f(mx, s0[r], s0[r + 1]);
-    mx = fmaxf(mx, s0[15]);
+    float mx = max16(s0);
     {
       const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
                                                        __builtin_bit_cast(uint32_t, mx), false, false);
@@ -886,14 +936,16 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       pb[0][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[j], c, -m_use));
       pb[1][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[8 + j], c, -m_use));
     }
-    float psum = 0.f;
+    // row sum from the fp16 values the PV product uses: two independent
+    // dot2 chains
+    float ps[2] = {0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
 #pragma unroll
       for (int j = 0; j < 8; j += 2)
-        psum = __builtin_amdgcn_fdot2(half2v{pb[st][j], pb[st][j + 1]}, ones, psum, false);
+        ps[st] = __builtin_amdgcn_fdot2(half2v{pb[st][j], pb[st][j + 1]}, ones, ps[st], false);
     }
-    l_run += psum;
+    l_run += ps[0] + ps[1];
 #pragma unroll
     for (int m = 0; m < NMF; ++m) {
       const int st = m / DBLK, i = m % DBLK;
