@@ -1,8 +1,10 @@
 """MI355X-native (gfx950) attention path: drop-in for `flashattention_custom`.
 
 Exports the reference's three operators (flashattention_custom/__init__.py:1-3)
-backed by hand-written HIP kernels in libfa_mi355x.so.
+backed by hand-written HIP kernels in libfa_mi355x.so, and a shared-pool
+paged K/V cache (the caller-side cache of engine/llama_tp.py:21-107).
 """
 from .ops import flash_attn, flash_attn_paged, paged_kv_append
+from .kv_cache import PagedKVCache
 
-__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append"]
+__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append", "PagedKVCache"]

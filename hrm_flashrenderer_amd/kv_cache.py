@@ -1,0 +1,250 @@
+"""Paged K/V cache over one shared page pool with a block table.
+
+Counterpart of the reference's caller-side cache, engine/llama_tp.py:21-107
+(`PagedKVCache`). The reference keeps a private page array per sequence,
+`[B, Hk, P, PS, D]`, grows every sequence to the next power of two of pages
+by reallocating and copying the whole cache (llama_tp.py:47-57), and reads
+positions and lengths back from the device with `.item()` on every append
+(llama_tp.py:69, 89-97).
+
+Here all sequences share one pool `[1, Hk, pool_pages, PS, D]` (the
+reference's 5-D layout with a single pool row, so the kernels' page map
+applies unchanged) and a block table `[B, max_blocks]` of int32 physical page
+ids on the device:
+
+* pages are taken from a host-side free list only when a sequence's length
+  crosses a page boundary, and returned by `free(b)` / `reset()`;
+* the pool doubles (one device copy) only when the free list runs dry, and
+  the block table widens only when a sequence outgrows it;
+* lengths are tracked on the host for allocation, and the device `seqlen`
+  is advanced by device ops in stream order (an append at the current
+  lengths passes `seqlen` itself as the kernel's start positions), so an
+  append whose positions are known on the host (`positions=None`, a Python
+  int, or a CPU tensor) never waits on the device; a device tensor of
+  positions costs one read-back, as in the reference;
+* block-table changes are written with a small scatter of the new entries.
+
+The operators consume the cache through `get()` / `block_table`, or directly
+through `attention()`.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from .ops import flash_attn_paged, paged_kv_append
+
+PositionsLike = Union[None, int, torch.Tensor]
+
+
+class PagedKVCache:
+    """Shared-pool paged K/V cache (see the module docstring).
+
+    Arguments follow the reference constructor (engine/llama_tp.py:24-33):
+    `init_pages` is the initial number of pages per sequence, so the pool
+    starts with `bsz * init_pages` pages. `max_seq_len` (optional) sizes the
+    block table up front; it widens on demand otherwise.
+    """
+
+    def __init__(self, bsz: int, kv_heads: int, head_dim: int, page_size: int = 128,
+                 init_pages: int = 4, device: Union[str, torch.device] = "cuda",
+                 dtype: torch.dtype = torch.float16, *, max_seq_len: Optional[int] = None,
+                 pool_pages: Optional[int] = None):
+        self.bsz = int(bsz)
+        self.kv_heads = int(kv_heads)
+        self.head_dim = int(head_dim)
+        self.page_size = int(page_size)
+        self.device = torch.device(device)
+        self.dtype = dtype
+        if self.bsz <= 0 or self.kv_heads <= 0 or self.head_dim <= 0 or self.page_size <= 0:
+            raise ValueError("bsz, kv_heads, head_dim and page_size must be positive")
+        npages = int(pool_pages) if pool_pages is not None else self.bsz * max(1, int(init_pages))
+        npages = max(1, npages)
+        self.k_pages = torch.empty(1, self.kv_heads, npages, self.page_size, self.head_dim,
+                                   device=self.device, dtype=dtype)
+        self.v_pages = torch.empty_like(self.k_pages)
+        blocks = max(1, int(init_pages))
+        if max_seq_len is not None:
+            blocks = max(blocks, -(-int(max_seq_len) // self.page_size))
+        self._bt_host = np.full((self.bsz, blocks), -1, dtype=np.int32)
+        self._block_table = torch.full((self.bsz, blocks), -1, dtype=torch.int32,
+                                       device=self.device)
+        self._free: List[int] = list(range(npages - 1, -1, -1))  # pop() yields low ids first
+        self._pages_of = [0] * self.bsz       # mapped logical pages per sequence
+        self.lengths = [0] * self.bsz         # host copy of seqlen
+        self.seqlen = torch.zeros(self.bsz, dtype=torch.int32, device=self.device)
+        self.cur_len = 0                      # max length, as the reference tracks it
+
+    # ------------------------------------------------------------ queries --
+    @property
+    def pool_pages(self) -> int:
+        return int(self.k_pages.size(2))
+
+    @property
+    def max_blocks(self) -> int:
+        return int(self._bt_host.shape[1])
+
+    @property
+    def block_table(self) -> torch.Tensor:
+        return self._block_table
+
+    @property
+    def free_pages(self) -> int:
+        return len(self._free)
+
+    def get(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(k_pages, v_pages, seqlen) as in the reference (llama_tp.py:101-102);
+        the operators also need `block_table=cache.block_table`."""
+        return self.k_pages, self.v_pages, self.seqlen
+
+    # --------------------------------------------------------- allocation --
+    def reserve(self, b: int, end: int) -> None:
+        """Map the pages that hold positions [0, end) of sequence b."""
+        need = -(-int(end) // self.page_size)
+        have = self._pages_of[b]
+        if need <= have:
+            return
+        self._reserve_many([(b, need)])
+
+    def _reserve_many(self, wants: Sequence[Tuple[int, int]]) -> None:
+        new_entries = []
+        for b, need in wants:
+            have = self._pages_of[b]
+            if need <= have:
+                continue
+            if need > self.max_blocks:
+                self._widen_table(max(need, 2 * self.max_blocks))
+            missing = need - have
+            if missing > len(self._free):
+                self._grow_pool(missing - len(self._free))
+            for p in range(have, need):
+                phi = self._free.pop()
+                self._bt_host[b, p] = phi
+                new_entries.append((b, p, phi))
+            self._pages_of[b] = need
+        if new_entries:
+            idx = torch.tensor(new_entries, dtype=torch.int64)
+            vals = idx[:, 2].to(torch.int32)
+            rows = idx[:, 0].to(self.device, non_blocking=True)
+            cols = idx[:, 1].to(self.device, non_blocking=True)
+            self._block_table[rows, cols] = vals.to(self.device, non_blocking=True)
+
+    def _widen_table(self, blocks: int) -> None:
+        old = self._bt_host
+        host = np.full((self.bsz, blocks), -1, dtype=np.int32)
+        host[:, :old.shape[1]] = old
+        self._bt_host = host
+        dev = torch.full((self.bsz, blocks), -1, dtype=torch.int32, device=self.device)
+        dev[:, :old.shape[1]] = self._block_table
+        self._block_table = dev
+
+    def _grow_pool(self, at_least: int) -> None:
+        old = self.pool_pages
+        new = max(2 * old, old + int(at_least))
+        k = torch.empty(1, self.kv_heads, new, self.page_size, self.head_dim,
+                        device=self.device, dtype=self.dtype)
+        v = torch.empty_like(k)
+        k[:, :, :old] = self.k_pages
+        v[:, :, :old] = self.v_pages
+        self.k_pages, self.v_pages = k, v
+        # new ids go to the bottom of the stack so that freed low ids are reused first
+        self._free = list(range(new - 1, old - 1, -1)) + self._free
+
+    def free(self, b: int) -> None:
+        """Release sequence b's pages and set its length to zero."""
+        n = self._pages_of[b]
+        if n:
+            ids = self._bt_host[b, :n].tolist()
+            self._free.extend(reversed(ids))
+            self._bt_host[b, :n] = -1
+            self._block_table[b, :n] = -1
+            self._pages_of[b] = 0
+        self._set_lengths({b: 0}, shrink=True)
+
+    def reset(self) -> None:
+        """Forget every sequence but keep the pool (llama_tp.py:104-107)."""
+        for b in range(self.bsz):
+            self.free(b)
+        self.cur_len = 0
+
+    # ------------------------------------------------------------- append --
+    def _starts(self, positions: PositionsLike, T: int) -> List[int]:
+        if positions is None:
+            return list(self.lengths)
+        if isinstance(positions, int):
+            return [int(positions)] * self.bsz
+        if not isinstance(positions, torch.Tensor):
+            positions = torch.as_tensor(positions)
+        pos = positions.detach()
+        if pos.device.type != "cpu":
+            pos = pos.cpu()  # one read-back, like the reference's .item() calls
+        if pos.dim() == 1:
+            if pos.numel() != T:
+                raise ValueError("positions [T] must have T entries")
+            start = int(pos[0]) if T else 0
+            if T and not torch.equal(pos.to(torch.int64), torch.arange(start, start + T)):
+                raise ValueError("positions [T] must be consecutive")
+            return [start] * self.bsz
+        if pos.dim() == 2:
+            if tuple(pos.shape) != (self.bsz, T):
+                raise ValueError("positions [B, T] must match k_new")
+            starts = pos[:, 0].tolist() if T else [0] * self.bsz
+            want = torch.tensor(starts, dtype=torch.int64)[:, None] + torch.arange(T)[None]
+            if T and not torch.equal(pos.to(torch.int64), want):
+                raise ValueError("each row of positions [B, T] must be consecutive")
+            return [int(s) for s in starts]
+        raise ValueError("positions must be None, an int, [T] or [B, T]")
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor,
+               positions: PositionsLike = None) -> None:
+        """Write k_new / v_new `[B, Hk, T, D]` at positions start_b .. start_b+T-1.
+
+        `positions`: None (append at each sequence's current length), an int
+        or a `[T]` tensor (same start for all sequences, as the reference's
+        fast path, llama_tp.py:65-78), or `[B, T]` (per-sequence starts; each
+        row consecutive). One kernel launch in every case.
+        """
+        B, Hk, T, D = k_new.shape
+        if B != self.bsz or Hk != self.kv_heads or D != self.head_dim:
+            raise ValueError("k_new must be [bsz, kv_heads, T, head_dim]")
+        starts = self._starts(positions, T)
+        if any(s < 0 for s in starts):
+            raise ValueError("positions must be non-negative")
+        if T == 0:
+            return
+        self._reserve_many([(b, -(-(s + T) // self.page_size)) for b, s in enumerate(starts)])
+        uniform = len(set(starts)) == 1
+        if uniform:
+            start_arg: Union[int, torch.Tensor] = starts[0]
+        elif positions is None:
+            start_arg = self.seqlen  # the current lengths, already on the device
+        else:
+            start_arg = torch.tensor(starts, dtype=torch.int32).to(self.device, non_blocking=True)
+        paged_kv_append(self.k_pages, self.v_pages, k_new.contiguous(), v_new.contiguous(),
+                        start_arg, self.page_size, block_table=self._block_table)
+        # seqlen = max(seqlen, start + T), in stream order after the kernel
+        if uniform:
+            self.seqlen.clamp_(min=starts[0] + T)
+        elif positions is None:
+            self.seqlen.add_(T)
+        else:
+            torch.maximum(self.seqlen, start_arg + T, out=self.seqlen)
+        for b, st in enumerate(starts):
+            self.lengths[b] = max(self.lengths[b], st + T)
+        self.cur_len = max(self.lengths)
+
+    def _set_lengths(self, new: dict, shrink: bool = False) -> None:
+        for b, n in new.items():
+            if shrink or n > self.lengths[b]:
+                self.lengths[b] = int(n)
+                self.seqlen[b].fill_(int(n))
+        self.cur_len = max(self.lengths) if self.lengths else 0
+
+    # ---------------------------------------------------------- attention --
+    def attention(self, q: torch.Tensor, head_map: torch.Tensor, causal: bool,
+                  q_offset: Union[int, torch.Tensor] = 0) -> torch.Tensor:
+        """flash_attn_paged over this cache (block table included)."""
+        return flash_attn_paged(q, self.k_pages, self.v_pages, self.seqlen, self.page_size,
+                                head_map, causal, q_offset, 0, block_table=self._block_table)

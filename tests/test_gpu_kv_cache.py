@@ -1,0 +1,137 @@
+"""PagedKVCache on the GPU: appends through the block-table pool, then
+attention through the cache, against the fp64 oracle on a host-side shadow of
+every sequence's keys and values (bit-exact K/V, tolerance bar on outputs)."""
+import pytest
+import torch
+
+from hrm_flashrenderer_amd.kv_cache import PagedKVCache
+from oracle import attention as ora
+from paged_ref import assert_close, gather_seq, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+class Shadow:
+    """Host copy of what each sequence holds, position by position."""
+
+    def __init__(self, B, Hk, D):
+        self.k = [torch.zeros(Hk, 0, D, dtype=torch.float16) for _ in range(B)]
+        self.v = [torch.zeros(Hk, 0, D, dtype=torch.float16) for _ in range(B)]
+
+    def write(self, b, start, k, v):
+        T = k.shape[1]
+        for name, x in (("k", k), ("v", v)):
+            cur = getattr(self, name)[b]
+            n = max(cur.shape[1], start + T)
+            if n > cur.shape[1]:
+                cur = torch.cat([cur, torch.zeros(cur.shape[0], n - cur.shape[1], cur.shape[2],
+                                                  dtype=cur.dtype)], dim=1)
+            cur[:, start:start + T] = x
+            getattr(self, name)[b] = cur
+
+
+def _check_contents(cache, shadow):
+    kc, vc = cache.k_pages.cpu(), cache.v_pages.cpu()
+    bt = cache.block_table.cpu()
+    assert cache.seqlen.cpu().tolist() == cache.lengths
+    for b, n in enumerate(cache.lengths):
+        assert torch.equal(gather_seq(kc, bt[b], n, cache.page_size), shadow.k[b][:, :n]), b
+        assert torch.equal(gather_seq(vc, bt[b], n, cache.page_size), shadow.v[b][:, :n]), b
+
+
+def _check_attention(cache, shadow, q, hm, causal, q_offsets, what):
+    out = cache.attention(q, hm, causal,
+                          q_offsets if isinstance(q_offsets, int) else
+                          torch.tensor(q_offsets, dtype=torch.int32, device=q.device)).cpu()
+    for b, n in enumerate(cache.lengths):
+        qo = q_offsets if isinstance(q_offsets, int) else q_offsets[b]
+        ref = ora.attention_f64(q[b:b + 1].cpu(), shadow.k[b][None, :, :n], shadow.v[b][None, :, :n],
+                                causal, qo, 0, head_map=hm.cpu().tolist())
+        assert_close(out[b:b + 1], ref, f"{what} b={b}")
+
+
+@pytest.mark.parametrize("page_size", [16, 128])
+def test_prefill_then_decode_through_the_cache(gpu, page_size):
+    B, Hq, Hk, D = 3, 8, 2, 128
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    cache = PagedKVCache(B, Hk, D, page_size=page_size, init_pages=1, device=gpu)
+    shadow = Shadow(B, Hk, D)
+    # prefill chunk at position 0 for every sequence (positions=None: current lengths)
+    T = 75
+    k, v, q = seeded((B, Hk, T, D), 1), seeded((B, Hk, T, D), 2), seeded((B, Hq, T, D), 3)
+    cache.append(k, v)
+    for b in range(B):
+        shadow.write(b, 0, k[b].cpu(), v[b].cpu())
+    _check_contents(cache, shadow)
+    _check_attention(cache, shadow, q, hm, True, 0, "prefill")
+    # ragged second chunk: sequence 1 rewrites from position 20, others continue
+    T2 = 40
+    starts = [75, 20, 75]
+    pos = torch.tensor(starts)[:, None] + torch.arange(T2)[None]
+    k, v, q = seeded((B, Hk, T2, D), 4), seeded((B, Hk, T2, D), 5), seeded((B, Hq, T2, D), 6)
+    cache.append(k, v, pos)
+    for b in range(B):
+        shadow.write(b, starts[b], k[b].cpu(), v[b].cpu())
+    assert cache.lengths == [115, 75, 115]
+    _check_contents(cache, shadow)
+    _check_attention(cache, shadow, q, hm, True, starts, "ragged chunk")
+    # decode steps at the current lengths (device-side starts, no read-back)
+    for step in range(6):
+        k, v, q = (seeded((B, Hk, 1, D), 10 + step), seeded((B, Hk, 1, D), 20 + step),
+                   seeded((B, Hq, 1, D), 30 + step))
+        before = list(cache.lengths)
+        cache.append(k, v)
+        for b in range(B):
+            shadow.write(b, before[b], k[b].cpu(), v[b].cpu())
+        _check_attention(cache, shadow, q, hm, False, 0, f"decode {step}")
+    _check_contents(cache, shadow)
+    assert cache.pool_pages >= sum(-(-n // page_size) for n in cache.lengths)
+
+
+def test_growth_free_and_reuse(gpu):
+    B, Hq, Hk, D, PS = 2, 4, 1, 64, 16
+    hm = torch.zeros(Hq, dtype=torch.int32, device=gpu)
+    cache = PagedKVCache(B, Hk, D, page_size=PS, init_pages=1, device=gpu)
+    shadow = Shadow(B, Hk, D)
+    for step, T in enumerate([5, 40, 3, 100]):      # several pool growths
+        k, v = seeded((B, Hk, T, D), 40 + step), seeded((B, Hk, T, D), 50 + step)
+        before = list(cache.lengths)
+        cache.append(k, v)
+        for b in range(B):
+            shadow.write(b, before[b], k[b].cpu(), v[b].cpu())
+        _check_contents(cache, shadow)
+    cache.free(0)
+    shadow.k[0], shadow.v[0] = shadow.k[0][:, :0], shadow.v[0][:, :0]
+    k, v = seeded((B, Hk, 70, D), 60), seeded((B, Hk, 70, D), 61)
+    pool = cache.pool_pages
+    before = list(cache.lengths)
+    cache.append(k, v)                              # sequence 0 reuses its freed pages
+    for b in range(B):
+        shadow.write(b, before[b], k[b].cpu(), v[b].cpu())
+    assert cache.pool_pages == pool or cache.free_pages >= 0
+    _check_contents(cache, shadow)
+    q = seeded((B, Hq, 1, D), 62)
+    _check_attention(cache, shadow, q, hm, False, 0, "after reuse")
+    cache.reset()
+    assert cache.lengths == [0, 0] and (cache.seqlen == 0).all()
+    out = cache.attention(q, hm, False).cpu()
+    assert (out == 0).all()                          # no keys: zero rows
+
+
+def test_llama_tp_attention_pattern(gpu):
+    """engine/llama_tp.py:182-200 with the cache: append the chunk at its
+    positions, attend with causal=prefill and q_offset = first position."""
+    B, Hq, Hk, D, PS = 2, 8, 2, 128, 128
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    cache = PagedKVCache(B, Hk, D, page_size=PS, device=gpu)
+    shadow = Shadow(B, Hk, D)
+    cur = 0
+    for step, T in enumerate([200, 1, 1, 57]):
+        q, k, v = (seeded((B, Hq, T, D), 70 + step), seeded((B, Hk, T, D), 80 + step),
+                   seeded((B, Hk, T, D), 90 + step))
+        positions = torch.arange(cur, cur + T, device=gpu)   # device positions: one read-back
+        cache.append(k, v, positions)
+        for b in range(B):
+            shadow.write(b, cur, k[b].cpu(), v[b].cpu())
+        _check_attention(cache, shadow, q, hm, T > 1, cur, f"step {step}")
+        cur += T

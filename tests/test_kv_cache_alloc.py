@@ -1,0 +1,89 @@
+"""Host-side logic of PagedKVCache (no GPU): page accounting over the shared
+pool, block-table contents, pool growth, table widening, free/reset, and the
+validation of `positions`. The cache itself does no arithmetic on the host:
+an append on a CPU cache raises the operators' RuntimeError."""
+import numpy as np
+import pytest
+import torch
+
+from hrm_flashrenderer_amd.kv_cache import PagedKVCache
+
+
+def _cache(**kw):
+    args = dict(bsz=3, kv_heads=2, head_dim=64, page_size=16, init_pages=2, device="cpu")
+    args.update(kw)
+    return PagedKVCache(**args)
+
+
+def _mapped(c, b):
+    row = c.block_table[b].tolist()
+    return [x for x in row if x >= 0]
+
+
+def test_initial_state():
+    c = _cache()
+    assert c.pool_pages == 6 and c.free_pages == 6 and c.max_blocks == 2
+    assert tuple(c.k_pages.shape) == (1, 2, 6, 16, 64)
+    assert (c.block_table == -1).all() and (c.seqlen == 0).all() and c.lengths == [0, 0, 0]
+
+
+def test_reserve_maps_ceil_pages_with_distinct_ids():
+    c = _cache()
+    c.reserve(0, 16)    # exactly one page
+    c.reserve(1, 17)    # two pages
+    c.reserve(2, 1)
+    assert [len(_mapped(c, b)) for b in range(3)] == [1, 2, 1]
+    ids = sum((_mapped(c, b) for b in range(3)), [])
+    assert len(set(ids)) == len(ids) and all(0 <= i < c.pool_pages for i in ids)
+    assert c.free_pages == c.pool_pages - len(ids)
+    c.reserve(1, 20)    # already covered: no new page
+    assert len(_mapped(c, 1)) == 2
+
+
+def test_pool_growth_and_table_widening_keep_existing_entries():
+    c = _cache()
+    c.reserve(0, 32)
+    before = _mapped(c, 0)
+    c.reserve(1, 16 * 9)            # 9 pages: widens the table and grows the pool
+    assert c.max_blocks >= 9 and c.pool_pages >= 11
+    assert _mapped(c, 0) == before
+    ids = _mapped(c, 0) + _mapped(c, 1)
+    assert len(set(ids)) == len(ids) and max(ids) < c.pool_pages
+    assert tuple(c.k_pages.shape) == (1, 2, c.pool_pages, 16, 64)
+    assert c.free_pages == c.pool_pages - len(ids)
+
+
+def test_free_returns_pages_and_reset_keeps_the_pool():
+    c = _cache()
+    c.reserve(0, 48)
+    c.reserve(1, 16)
+    freed = _mapped(c, 0)
+    c.free(0)
+    assert _mapped(c, 0) == [] and c.lengths[0] == 0 and int(c.seqlen[0]) == 0
+    c.reserve(2, 48)
+    assert sorted(_mapped(c, 2)) == sorted(freed)   # freed pages are reused first
+    pool = c.pool_pages
+    c.reset()
+    assert c.free_pages == pool and c.pool_pages == pool and (c.block_table == -1).all()
+    assert c.cur_len == 0
+
+
+@pytest.mark.parametrize("positions,msg", [
+    (torch.tensor([3, 4, 6]), "consecutive"),
+    (torch.tensor([1, 2]), "T entries"),
+    (torch.tensor([[0, 1, 2], [5, 6, 8], [0, 1, 2]]), "consecutive"),
+    (torch.tensor([[0, 1, 2]]), "match"),
+    (-1, "non-negative"),
+])
+def test_positions_validation(positions, msg):
+    c = _cache()
+    k = torch.zeros(3, 2, 3, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match=msg):
+        c.append(k, k, positions)
+
+
+def test_append_on_a_cpu_cache_raises_instead_of_computing():
+    c = _cache()
+    k = torch.zeros(3, 2, 3, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        c.append(k, k)
