@@ -146,12 +146,13 @@ size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacit
   return fa::plan_decode(B, Hq, M, D, Hk, cap).ws_bytes;
 }
 
-int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
-                            const int32_t* seqlen, int page_size, const int32_t* head_map, void* o,
-                            int B, int Hq, int M, int D, int NB, int Hk, int P, int causal,
-                            int64_t q_offset, int64_t k_offset, const int32_t* q_offsets,
-                            const int32_t* k_offsets, const int32_t* block_table, int max_blocks,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
+                     const int32_t* seqlen, int page_size, const int32_t* head_map, void* o, int B,
+                     int Hq, int M, int D, int NB, int Hk, int P, int causal, int64_t q_offset,
+                     int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
+                     const int32_t* block_table, int max_blocks, void* workspace,
+                     size_t workspace_bytes, const void* rope_cos, const void* rope_sin,
+                     int rope_len, void* stream) {
   if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
   int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
   if (rc != FA_OK) return rc;
@@ -182,6 +183,9 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
   p.q_offset = narrow(q_offset);
   p.k_offset = narrow(k_offset);
   p.scale_log2 = fa::kLog2e / sqrtf((float)D);
+  p.rope_cos = reinterpret_cast<const fa::f16*>(rope_cos);
+  p.rope_sin = reinterpret_cast<const fa::f16*>(rope_sin);
+  p.rope_len = rope_len;
 
   (void)hipGetLastError();
   if (fa::use_decode_path(B, M, Hq, Hk)) {
@@ -200,22 +204,70 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
   return launch_status(fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream));
 }
 
-int fa_paged_kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
-                       int Hk, int T, int D, int NB, int P, int page_size, int64_t start_pos,
-                       const int32_t* start_positions, const int32_t* block_table, int max_blocks,
-                       void* stream) {
+int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
+                            const int32_t* seqlen, int page_size, const int32_t* head_map, void* o,
+                            int B, int Hq, int M, int D, int NB, int Hk, int P, int causal,
+                            int64_t q_offset, int64_t k_offset, const int32_t* q_offsets,
+                            const int32_t* k_offsets, const int32_t* block_table, int max_blocks,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
+                   causal, q_offset, k_offset, q_offsets, k_offsets, block_table, max_blocks,
+                   workspace, workspace_bytes, nullptr, nullptr, 0, stream);
+}
+
+int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void* v_pages,
+                                 const int32_t* seqlen, int page_size, const int32_t* head_map,
+                                 void* o, int B, int Hq, int M, int D, int NB, int Hk, int P,
+                                 int causal, int64_t q_offset, int64_t k_offset,
+                                 const int32_t* q_offsets, const int32_t* k_offsets,
+                                 const int32_t* block_table, int max_blocks, void* workspace,
+                                 size_t workspace_bytes, const void* rope_cos,
+                                 const void* rope_sin, int rope_len, void* stream) {
+  if (rope_cos == nullptr || rope_sin == nullptr || rope_len <= 0)
+    return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
+  return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
+                   causal, q_offset, k_offset, q_offsets, k_offsets, block_table, max_blocks,
+                   workspace, workspace_bytes, rope_cos, rope_sin, rope_len, stream);
+}
+
+static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
+                     int Hk, int T, int D, int NB, int P, int page_size, int64_t start_pos,
+                     const int32_t* start_positions, const int32_t* block_table, int max_blocks,
+                     const void* rope_cos, const void* rope_sin, int rope_len, void* stream) {
   if (B < 0 || T < 0 || D <= 0) return fail(FA_ERR_INVALID, "shape mismatch");
   int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
   if (rc != FA_OK) return rc;
   if (D % 8 != 0) return fail(FA_ERR_INVALID, "head_dim must be a multiple of 8");
+  if (rope_cos != nullptr && D % 16 != 0)
+    return fail(FA_ERR_INVALID, "rotary append needs head_dim a multiple of 16");
   if ((int64_t)B * Hk * T == 0) return FA_OK;
   if (k_pages == nullptr || v_pages == nullptr || k_new == nullptr || v_new == nullptr)
     return fail(FA_ERR_INVALID, "null tensor pointer");
   const fa::KVMap map = paged_map(block_table, max_blocks, NB, Hk, P, page_size, D);
   (void)hipGetLastError();
-  return launch_status(fa::launch_paged_append(k_pages, v_pages, k_new, v_new, map, B, Hk, T,
-                                               narrow(start_pos), start_positions,
-                                               (hipStream_t)stream));
+  return launch_status(fa::launch_paged_append(
+      k_pages, v_pages, k_new, v_new, map, B, Hk, T, narrow(start_pos), start_positions,
+      reinterpret_cast<const fa::f16*>(rope_cos), reinterpret_cast<const fa::f16*>(rope_sin),
+      rope_len, (hipStream_t)stream));
+}
+
+int fa_paged_kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
+                       int Hk, int T, int D, int NB, int P, int page_size, int64_t start_pos,
+                       const int32_t* start_positions, const int32_t* block_table, int max_blocks,
+                       void* stream) {
+  return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, start_pos,
+                   start_positions, block_table, max_blocks, nullptr, nullptr, 0, stream);
+}
+
+int fa_paged_kv_append_rope(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
+                            int B, int Hk, int T, int D, int NB, int P, int page_size,
+                            int64_t start_pos, const int32_t* start_positions,
+                            const int32_t* block_table, int max_blocks, const void* rope_cos,
+                            const void* rope_sin, int rope_len, void* stream) {
+  if (rope_cos == nullptr || rope_sin == nullptr || rope_len <= 0)
+    return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
+  return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, start_pos,
+                   start_positions, block_table, max_blocks, rope_cos, rope_sin, rope_len, stream);
 }
 
 }  // extern "C"

@@ -52,16 +52,78 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
   *reinterpret_cast<u32x4*>(v_pages + dst) = vv;
 }
 
+// Append with the rotary embedding of K fused in (the reference applies
+// engine/rope.py:15-24 to K before llama_tp.py:74 appends it). One lane takes
+// the 8-element chunk c < D/16 of a row together with its rotary partner
+// c + D/16: it rotates and writes both K chunks and copies both V chunks.
+// A position outside the rotary table writes NaN keys.
+__global__ __launch_bounds__(256) void paged_append_rope_kernel(
+    f16* __restrict__ k_pages, f16* __restrict__ v_pages,
+    const f16* __restrict__ k_new, const f16* __restrict__ v_new,
+    KVMap map, int B, int Hk, int T, int pairs_per_row, int start_pos,
+    const int32_t* __restrict__ start_positions, const f16* __restrict__ rope_cos,
+    const f16* __restrict__ rope_sin, int rope_len, int64_t total_pairs) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total_pairs) return;
+  const int64_t row = idx / pairs_per_row;
+  const int pair = (int)(idx - row * pairs_per_row);
+  const int t = (int)(row % T);
+  const int64_t bh = row / T;
+  const int hk = (int)(bh % Hk);
+  const int b = (int)(bh / Hk);
+
+  const int start = start_positions ? start_positions[b] : start_pos;
+  const int pos = start + t;
+  if (pos < 0) return;
+  const int64_t dst_row = map.row_offset(b, hk, pos);
+  if (dst_row < 0) return;
+
+  const int half = map.D / 2;
+  const int64_t src = row * map.D + pair * 8;
+  const int64_t dst = dst_row + pair * 8;
+  const half8 x1 = *reinterpret_cast<const half8*>(k_new + src);
+  const half8 x2 = *reinterpret_cast<const half8*>(k_new + src + half);
+  const bool ok = pos < rope_len;
+  const int64_t trow = (int64_t)(ok ? pos : 0) * half + pair * 8;
+  const half8 c = *reinterpret_cast<const half8*>(rope_cos + trow);
+  const half8 s = *reinterpret_cast<const half8*>(rope_sin + trow);
+  half8 y1, y2;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    f16 a, e;
+    rope_pair(x1[j], x2[j], c[j], s[j], a, e);
+    y1[j] = ok ? a : (f16)__builtin_nanf("");
+    y2[j] = ok ? e : (f16)__builtin_nanf("");
+  }
+  *reinterpret_cast<half8*>(k_pages + dst) = y1;
+  *reinterpret_cast<half8*>(k_pages + dst + half) = y2;
+  *reinterpret_cast<u32x4*>(v_pages + dst) = *reinterpret_cast<const u32x4*>(v_new + src);
+  *reinterpret_cast<u32x4*>(v_pages + dst + half) = *reinterpret_cast<const u32x4*>(v_new + src + half);
+}
+
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
-                               const int32_t* start_positions, hipStream_t stream) {
+                               const int32_t* start_positions, const f16* rope_cos,
+                               const f16* rope_sin, int rope_len, hipStream_t stream) {
+  const int threads = 256;
+  if (rope_cos != nullptr) {
+    const int pairs_per_row = map.D / 16;
+    const int64_t total = (int64_t)B * Hk * T * pairs_per_row;
+    if (total == 0) return hipSuccess;
+    const int64_t blocks = (total + threads - 1) / threads;
+    hipLaunchKernelGGL(paged_append_rope_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
+                       reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
+                       reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new),
+                       map, B, Hk, T, pairs_per_row, start_pos, start_positions, rope_cos,
+                       rope_sin, rope_len, total);
+    return hipGetLastError();
+  }
   const int chunks_per_row = map.D / 8;
   int chunk_shift = 0;
   while ((1 << chunk_shift) < chunks_per_row) ++chunk_shift;
   if ((1 << chunk_shift) != chunks_per_row) chunk_shift = -1;
   const int64_t total = (int64_t)B * Hk * T * chunks_per_row;
   if (total == 0) return hipSuccess;
-  const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
   hipLaunchKernelGGL(paged_append_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
                      reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),

@@ -102,6 +102,11 @@ struct AttnParams {
   int* ws_units;        // [B + 1] units (16-key groups x Hk) before sequence b
   int dec_wgs;          // workgroups of the decode kernel
   int dec_rows;         // row capacity of a slot: Hq * M
+  // optional rotary embedding of Q at load time (nullptr: none): fp16 tables
+  // [rope_len, D/2]; query row i of sequence b sits at position q_off(b) + i
+  const f16* rope_cos;
+  const f16* rope_sin;
+  int rope_len;
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
@@ -120,10 +125,50 @@ struct AttnParams {
   }
 };
 
+// One rotary pair in the fp16 operation order of the reference's apply_rope
+// (engine/rope.py:15-24, half-split layout): y1 = x1*c - x2*s, y2 = x1*s + x2*c
+// with every product and the sum rounded to fp16. Each step is one fp32
+// operation rounded to fp16; fp32 carries more than 2*11+2 bits, so this is
+// the correctly rounded fp16 operation, the same result torch's fp16 ops give.
+__device__ __forceinline__ void rope_pair(f16 x1, f16 x2, f16 c, f16 s, f16& y1, f16& y2) {
+  // each product is rounded before the sum: no fused multiply-add
+#pragma clang fp contract(off)
+  const f16 a = (f16)((float)x1 * (float)c);
+  const f16 b = (f16)((float)x2 * (float)s);
+  const f16 e = (f16)((float)x1 * (float)s);
+  const f16 f = (f16)((float)x2 * (float)c);
+  y1 = (f16)((float)a - (float)b);
+  y2 = (f16)((float)e + (float)f);
+}
+
+// Rotary embedding of the query fragment a lane holds: q[i] holds dims
+// base + STRIDE*i + (0..7) of one query row, N*STRIDE == D, so the partner
+// d + D/2 of a dim d < D/2 is in q[i + N/2] at the same element. Rows at a
+// position outside the table become NaN.
+template <int N, int STRIDE>
+__device__ __forceinline__ void rope_fragment(half8* q, const AttnParams& p, int pos, int base) {
+  constexpr int HALF = N * STRIDE / 2;
+  const bool ok = pos >= 0 && pos < p.rope_len;
+  const int64_t row = (int64_t)(ok ? pos : 0) * HALF + base;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const half8 c = *reinterpret_cast<const half8*>(p.rope_cos + row + STRIDE * i);
+    const half8 s = *reinterpret_cast<const half8*>(p.rope_sin + row + STRIDE * i);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      f16 y1, y2;
+      rope_pair(q[i][j], q[i + N / 2][j], c[j], s[j], y1, y2);
+      q[i][j] = ok ? y1 : (f16)__builtin_nanf("");
+      q[i + N / 2][j] = ok ? y2 : (f16)__builtin_nanf("");
+    }
+  }
+}
+
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
-                               const int32_t* start_positions, hipStream_t stream);
+                               const int32_t* start_positions, const f16* rope_cos,
+                               const f16* rope_sin, int rope_len, hipStream_t stream);
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream);
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
 

@@ -304,6 +304,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
       }
+      if (p.rope_cos != nullptr && row_ok) rope_fragment<KSTEPS, 32>(qreg, p, qo + qi, 8 * quarter);
 
       float m_ref = -INFINITY;  // scaled (log2) reference max of the row
       float l_run = 0.f;

@@ -213,6 +213,7 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
                    ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
                    : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
+  if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
   floatx16 acc_o[DBLK];
 #pragma unroll
@@ -599,6 +600,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_pipe_kernel(AttnParams p,
                    ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
                    : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
+  if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
   int koff[KSTEPS];
 #pragma unroll
@@ -848,6 +850,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
                    ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
                    : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
+  if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
   // LDS byte offsets of the lane's operands. K: row col, logical chunk
   // 2*ks + half_id at chunk ^ swz_k(col); the chunk bits of 2*ks and half_id

@@ -198,13 +198,15 @@ class PagedKVCache:
         raise ValueError("positions must be None, an int, [T] or [B, T]")
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor,
-               positions: PositionsLike = None) -> None:
+               positions: PositionsLike = None, *, rope=None) -> None:
         """Write k_new / v_new `[B, Hk, T, D]` at positions start_b .. start_b+T-1.
 
         `positions`: None (append at each sequence's current length), an int
         or a `[T]` tensor (same start for all sequences, as the reference's
         fast path, llama_tp.py:65-78), or `[B, T]` (per-sequence starts; each
-        row consecutive). One kernel launch in every case.
+        row consecutive). One kernel launch in every case. `rope=(cos, sin)`
+        rotates the keys at their positions in the same launch (the
+        reference's apply_rope on K, engine/llama_tp.py:183).
         """
         B, Hk, T, D = k_new.shape
         if B != self.bsz or Hk != self.kv_heads or D != self.head_dim:
@@ -223,7 +225,7 @@ class PagedKVCache:
         else:
             start_arg = torch.tensor(starts, dtype=torch.int32).to(self.device, non_blocking=True)
         paged_kv_append(self.k_pages, self.v_pages, k_new.contiguous(), v_new.contiguous(),
-                        start_arg, self.page_size, block_table=self._block_table)
+                        start_arg, self.page_size, block_table=self._block_table, rope=rope)
         # seqlen = max(seqlen, start + T), in stream order after the kernel
         if uniform:
             self.seqlen.clamp_(min=starts[0] + T)
@@ -244,7 +246,9 @@ class PagedKVCache:
 
     # ---------------------------------------------------------- attention --
     def attention(self, q: torch.Tensor, head_map: torch.Tensor, causal: bool,
-                  q_offset: Union[int, torch.Tensor] = 0) -> torch.Tensor:
-        """flash_attn_paged over this cache (block table included)."""
+                  q_offset: Union[int, torch.Tensor] = 0, *, rope=None) -> torch.Tensor:
+        """flash_attn_paged over this cache (block table included); `rope`
+        rotates q in the kernel at positions q_offset + i."""
         return flash_attn_paged(q, self.k_pages, self.v_pages, self.seqlen, self.page_size,
-                                head_map, causal, q_offset, 0, block_table=self._block_table)
+                                head_map, causal, q_offset, 0, block_table=self._block_table,
+                                rope=rope)

@@ -26,6 +26,11 @@ behaviour):
     k_pages[phi // P, :, phi % P]. With it, k_pages.size(0) need not be B.
   * `flash_attn` also accepts fp32 q/k/v (fp32 arithmetic) and GQA
     (k.size(1) dividing q.size(1); q head h reads K/V head h // (Hq // Hk)).
+  * `rope=(cos, sin)` (fp16 [L, D/2] tables, engine/rope.py:6-13) on
+    `flash_attn_paged` rotates each query row at its position q_offset + i
+    as it is loaded, and on `paged_kv_append` rotates each key row at its
+    position before it is written: engine/rope.py:15-24's apply_rope fused
+    into the kernels, bit-identical to it.
 """
 from __future__ import annotations
 
@@ -100,6 +105,23 @@ def _check_block_table(block_table: Optional[torch.Tensor], B: int, device: torc
     return int(block_table.size(1))
 
 
+def _check_rope(rope, D: int, device: torch.device, require_device: bool = True):
+    """(cos, sin) fp16 tables [L, D/2] on the tensors' device, or None."""
+    if rope is None:
+        return None, None
+    _check(isinstance(rope, (tuple, list)) and len(rope) == 2, "rope must be (cos, sin)")
+    cos, sin = rope
+    _check(isinstance(cos, torch.Tensor) and isinstance(sin, torch.Tensor), "rope must be (cos, sin)")
+    if require_device:
+        _check(cos.is_cuda and sin.is_cuda, "CUDA required")
+    _check(cos.dtype == torch.float16 and sin.dtype == torch.float16, "rope tables fp16 required")
+    _check(cos.is_contiguous() and sin.is_contiguous(), "contiguous required")
+    _check(cos.dim() == 2 and cos.shape == sin.shape and cos.size(1) * 2 == D and cos.size(0) > 0,
+           "rope tables cos/sin [L, D/2] required")
+    _check(cos.device == device and sin.device == device, "tensors must be on one device")
+    return cos, sin
+
+
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -135,7 +157,8 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
                          seqlen: torch.Tensor, page_size: int, head_map: torch.Tensor,
                          causal: bool, q_offset: int, k_offset: int,
                          q_offsets: Optional[torch.Tensor], k_offsets: Optional[torch.Tensor],
-                         block_table: Optional[torch.Tensor]) -> torch.Tensor:
+                         block_table: Optional[torch.Tensor], rope_cos: Optional[torch.Tensor],
+                         rope_sin: Optional[torch.Tensor]) -> torch.Tensor:
     lib = _lib.load()
     o = torch.empty_like(q)
     B, Hq, M, D = q.shape
@@ -145,37 +168,47 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
     ws_bytes = lib.fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with _DeviceScope(q) as stream:
-        _lib.check(lib.fa_flash_attn_paged_fwd(
-            q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(), page_size,
-            head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P, int(causal),
-            q_offset, k_offset, _ptr(q_offsets), _ptr(k_offsets), _ptr(block_table), max_blocks,
-            _ptr(ws), ws_bytes, stream))
+        args = (q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(),
+                page_size, head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P,
+                int(causal), q_offset, k_offset, _ptr(q_offsets), _ptr(k_offsets),
+                _ptr(block_table), max_blocks, _ptr(ws), ws_bytes)
+        if rope_cos is None:
+            _lib.check(lib.fa_flash_attn_paged_fwd(*args, stream))
+        else:
+            _lib.check(lib.fa_flash_attn_paged_rope_fwd(
+                *args, rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.size(0), stream))
     return o
 
 
 @_flash_attn_paged_op.register_fake
 def _(q, k_pages, v_pages, seqlen, page_size, head_map, causal, q_offset, k_offset, q_offsets,
-      k_offsets, block_table):
+      k_offsets, block_table, rope_cos, rope_sin):
     return torch.empty_like(q)
 
 
 @torch.library.custom_op("hrm_fa::paged_kv_append", mutates_args=("k_pages", "v_pages"))
 def _paged_kv_append_op(k_pages: torch.Tensor, v_pages: torch.Tensor, k_new: torch.Tensor,
                         v_new: torch.Tensor, start_pos: int, start_positions: Optional[torch.Tensor],
-                        page_size: int, block_table: Optional[torch.Tensor]) -> None:
+                        page_size: int, block_table: Optional[torch.Tensor],
+                        rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor]) -> None:
     lib = _lib.load()
     B, Hk, T, D = k_new.shape
     NB, P = k_pages.size(0), k_pages.size(2)
     max_blocks = int(block_table.size(1)) if block_table is not None else 0
     with _DeviceScope(k_pages) as stream:
-        _lib.check(lib.fa_paged_kv_append(
-            k_pages.data_ptr(), v_pages.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
-            B, Hk, T, D, NB, P, page_size, start_pos, _ptr(start_positions),
-            _ptr(block_table), max_blocks, stream))
+        args = (k_pages.data_ptr(), v_pages.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+                B, Hk, T, D, NB, P, page_size, start_pos, _ptr(start_positions),
+                _ptr(block_table), max_blocks)
+        if rope_cos is None:
+            _lib.check(lib.fa_paged_kv_append(*args, stream))
+        else:
+            _lib.check(lib.fa_paged_kv_append_rope(
+                *args, rope_cos.data_ptr(), rope_sin.data_ptr(), rope_cos.size(0), stream))
 
 
 @_paged_kv_append_op.register_fake
-def _(k_pages, v_pages, k_new, v_new, start_pos, start_positions, page_size, block_table):
+def _(k_pages, v_pages, k_new, v_new, start_pos, start_positions, page_size, block_table,
+      rope_cos, rope_sin):
     return None
 
 
@@ -243,20 +276,27 @@ def validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
 
 
 def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
-                     causal=True, q_offset=0, k_offset=0, *, block_table=None):
+                     causal=True, q_offset=0, k_offset=0, *, block_table=None, rope=None):
     """Attention of q over paged K/V (prefill chunk or decode).
 
     Reference: flashattention_custom/ops.py:85-92 -> csrc/ext.cpp:42-68.
     q [B,Hq,M,D] fp16; k_pages/v_pages [NB,Hk,P,PS,D] fp16; seqlen int32 [B];
-    head_map int32 [Hq]. Returns a new tensor shaped like q.
+    head_map int32 [Hq]. Returns a new tensor shaped like q. With
+    rope=(cos, sin), q is rotated in the kernel (engine/rope.py:15-24) at
+    positions q_offset + i; a scalar q_offset must keep them inside the table.
     """
     page_size = int(page_size)
     validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
     B = q.size(0)
     qo, qo_t = _per_seq(q_offset, B, "q_offset", q.device)
     ko, ko_t = _per_seq(k_offset, B, "k_offset", q.device)
+    cos, sin = _check_rope(rope, q.size(3), q.device)
+    if cos is not None and qo_t is None and q.size(2) > 0:
+        _check(qo >= 0 and qo + q.size(2) <= cos.size(0),
+               f"positions {qo}..{qo + q.size(2) - 1} are outside the rotary table "
+               f"of {cos.size(0)}")
     return _flash_attn_paged_op(q, k_pages, v_pages, seqlen, page_size, head_map, bool(causal),
-                                qo, ko, qo_t, ko_t, block_table)
+                                qo, ko, qo_t, ko_t, block_table, cos, sin)
 
 
 def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
@@ -291,15 +331,25 @@ def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_siz
     return sp, sp_t
 
 
-def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, block_table=None):
+def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, block_table=None,
+                    rope=None):
     """Write k_new/v_new [B,Hk,T,D] at positions start_pos + t of each sequence, in place.
 
     Reference: flashattention_custom/ops.py:95-99 -> csrc/ext.cpp:70-89.
     A Python-int start_pos is range-checked against the page capacity and
     raises; per-sequence (tensor) starts skip out-of-range positions on the
     device, as the reference kernel does (csrc/flash_attn_sm75.cu:548).
+    With rope=(cos, sin) each key row is rotated at its position before it is
+    written (engine/rope.py:15-24; D a multiple of 16).
     """
     page_size = int(page_size)
     sp, sp_t = validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
                                         block_table)
-    _paged_kv_append_op(k_pages, v_pages, k_new, v_new, sp, sp_t, page_size, block_table)
+    cos, sin = _check_rope(rope, k_new.size(3), k_new.device)
+    if cos is not None:
+        _check(k_new.size(3) % 16 == 0, "rotary append needs head_dim a multiple of 16")
+        if sp_t is None and k_new.size(2) > 0:
+            _check(sp + k_new.size(2) <= cos.size(0),
+                   f"positions {sp}..{sp + k_new.size(2) - 1} are outside the rotary table "
+                   f"of {cos.size(0)}")
+    _paged_kv_append_op(k_pages, v_pages, k_new, v_new, sp, sp_t, page_size, block_table, cos, sin)

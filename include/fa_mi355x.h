@@ -121,6 +121,42 @@ int fa_paged_kv_append(void* k_pages, void* v_pages,
                        const int32_t* block_table, int max_blocks,
                        void* stream);
 
+/*
+ * fa_flash_attn_paged_fwd with the rotary embedding of Q applied at load
+ * time: query row i of sequence b is rotated at position q_off(b) + i by the
+ * half-split rule of engine/rope.py:15-24 (y1 = x1*c - x2*s, y2 = x1*s + x2*c
+ * over the halves x1 = q[:D/2], x2 = q[D/2:], each product and sum rounded to
+ * fp16 in the reference's order). Fuses the reference's apply_rope(q, ...)
+ * (engine/llama_tp.py:182-183) into the attention prologue.
+ *   rope_cos, rope_sin : fp16 [rope_len, D/2] (build_rope_cache, rope.py:6-13).
+ * A row whose position is outside [0, rope_len) yields NaN.
+ */
+int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void* v_pages,
+                                 const int32_t* seqlen, int page_size,
+                                 const int32_t* head_map, void* o,
+                                 int B, int Hq, int M, int D, int NB, int Hk, int P,
+                                 int causal, int64_t q_offset, int64_t k_offset,
+                                 const int32_t* q_offsets, const int32_t* k_offsets,
+                                 const int32_t* block_table, int max_blocks,
+                                 void* workspace, size_t workspace_bytes,
+                                 const void* rope_cos, const void* rope_sin, int rope_len,
+                                 void* stream);
+
+/*
+ * fa_paged_kv_append with the rotary embedding of K fused in: the key row of
+ * token t is rotated at its position start + t (same rule and tables as
+ * above; D % 16 == 0) before it is written; V is copied unchanged. Fuses
+ * apply_rope(k, ...) and cache.append (engine/llama_tp.py:183-186) into one
+ * pass. Keys at a position outside [0, rope_len) are written as NaN.
+ */
+int fa_paged_kv_append_rope(void* k_pages, void* v_pages,
+                            const void* k_new, const void* v_new,
+                            int B, int Hk, int T, int D, int NB, int P, int page_size,
+                            int64_t start_pos, const int32_t* start_positions,
+                            const int32_t* block_table, int max_blocks,
+                            const void* rope_cos, const void* rope_sin, int rope_len,
+                            void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* fa_last_error(void);
 

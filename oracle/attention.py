@@ -9,9 +9,10 @@ Contents
      (outputs within 2e-3 + 1e-2*|ref| of the exact softmax attention).
        attention_f64            O = softmax(Q K^T / sqrt(D) + mask) V
   2. Page-map helpers (numpy): the reference's paged layout and the additive
-     block-table indirection.
+     block-table indirection; the rotary embedding the fused kernels apply.
        gather_kv                pages -> contiguous [B, Hk, cap, D]
        append_f16               closed-form index map of paged_kv_append
+       rope_tables, rope_f16    engine/rope.py:6-24 (tables; fp16 apply_rope)
   3. Restatement of the reference's CPU math path (torch, same operation
      sequence and dtypes as flashattention_custom/ops.py:19-72), the "port"
      timed as the CPU baseline; pinned bit-for-bit by the golden vectors in
@@ -30,6 +31,12 @@ How each function is pinned (tests/test_oracle.py):
   append_f16        the reference's append known-answer test shape
                     (flash_tests/test_append_fast.py:16-38) against an
                     independent per-element loop; page-crossing starts.
+  rope_f16          bit-exact against torch's own fp16 CPU arithmetic on the
+                    same expression; position 0 is the identity; each
+                    rotated pair keeps its norm; rotating by p1 then p2
+                    matches rotating by p1 + p2; a planted sign error fails.
+  rope_tables       against the closed form cos/sin of t * theta^(-j/half)
+                    in float64 (to fp16 rounding).
   cpu_*             golden vectors written by the reference's own ops.py.
 """
 from __future__ import annotations
@@ -189,6 +196,40 @@ def append_f16(k_pages: ArrayLike, v_pages: ArrayLike, k_new: ArrayLike, v_new: 
             kp[phi // P, :, phi % P, slot[t]] = kn[b, :, t]
             vp[phi // P, :, phi % P, slot[t]] = vn[b, :, t]
     return kp, vp
+
+
+def rope_tables(max_len: int, head_dim: int, theta: float = 10000.0):
+    """cos/sin fp16 tables [max_len, D/2] as engine/rope.py:6-13 builds them:
+    inv_freq_j = theta^(-j/half), angle = t * inv_freq_j in fp32, then cos/sin
+    rounded to fp16. Returns numpy float16 arrays."""
+    half = head_dim // 2
+    inv = 1.0 / (np.float32(theta) ** (np.arange(half, dtype=np.float32) / np.float32(half)))
+    ang = np.arange(max_len, dtype=np.float32)[:, None] * inv.astype(np.float32)[None, :]
+    return np.cos(ang).astype(np.float16), np.sin(ang).astype(np.float16)
+
+
+def rope_f16(x: ArrayLike, cos: ArrayLike, sin: ArrayLike, positions) -> np.ndarray:
+    """apply_rope of engine/rope.py:15-24 in its fp16 operation order.
+
+    x [..., T, D] fp16 with the half-split layout x1 = x[..., :D/2],
+    x2 = x[..., D/2:]; c = cos[positions], s = sin[positions] ([T, D/2], or
+    [..., T, D/2] for per-row positions); y1 = x1*c - x2*s, y2 = x1*s + x2*c,
+    where every product and every sum is rounded to fp16 (torch's fp16 ops
+    compute in fp32 and round once; fp32 holds the product of two fp16 values
+    exactly). Returns float16.
+    """
+    xv = _np(x).astype(np.float16)
+    D = xv.shape[-1]
+    half = D // 2
+    pos = np.asarray(positions, dtype=np.int64)
+    c = _np(cos).astype(np.float16)[pos].astype(np.float32)
+    s = _np(sin).astype(np.float16)[pos].astype(np.float32)
+    x1 = xv[..., :half].astype(np.float32)
+    x2 = xv[..., half:].astype(np.float32)
+    r = lambda v: v.astype(np.float16).astype(np.float32)  # noqa: E731
+    y1 = (r(x1 * c) - r(x2 * s)).astype(np.float16)
+    y2 = (r(x1 * s) + r(x2 * c)).astype(np.float16)
+    return np.concatenate([y1, y2], axis=-1)
 
 
 # --------------------------------------------------------------------------

@@ -30,8 +30,9 @@ def declared_functions():
 
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
-        "fa_abi_version", "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd", "fa_last_error",
-        "fa_paged_kv_append", "fa_paged_workspace_bytes"])
+        "fa_abi_version", "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd",
+        "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
+        "fa_paged_kv_append_rope", "fa_paged_workspace_bytes"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -72,6 +73,17 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     rc, msg = _status_and_message(lib.fa_paged_kv_append(
         P, P, P, P, 2, 4, 3, 12, 2, 4, 16, 0, None, None, 0, None))
     assert rc == -1 and msg == "head_dim must be a multiple of 8"
+    # rotary variants: tables required; the fused append needs D % 16 == 0
+    rc, msg = _status_and_message(lib.fa_flash_attn_paged_rope_fwd(
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0,
+        None, None, 0, None))
+    assert rc == -1 and msg == "rotary tables cos/sin [L, D/2] required"
+    rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
+        P, P, P, P, 2, 4, 3, 128, 2, 4, 16, 0, None, None, 0, None, None, 0, None))
+    assert rc == -1 and msg == "rotary tables cos/sin [L, D/2] required"
+    rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
+        P, P, P, P, 2, 4, 3, 24, 2, 4, 16, 0, None, None, 0, P, P, 64, None))
+    assert rc == -1 and msg == "rotary append needs head_dim a multiple of 16"
     # empty work returns OK without any launch
     assert lib.fa_flash_attn_fwd(P, P, P, P, 0, 0, 8, 8, 16, 16, 64, 1, 0, 0, None, None, None) == 0
     assert lib.fa_paged_kv_append(P, P, P, P, 2, 4, 0, 128, 2, 4, 16, 0, None, None, 0, None) == 0
@@ -220,12 +232,18 @@ def test_custom_ops_have_shape_functions():
     kp = torch.empty(2, 2, 4, 16, 128, dtype=torch.float16, device="meta")
     sl = torch.empty(2, dtype=torch.int32, device="meta")
     hm = torch.empty(8, dtype=torch.int32, device="meta")
-    o = torch.ops.hrm_fa.flash_attn_paged(q, kp, kp, sl, 16, hm, True, 0, 0, None, None, None)
+    o = torch.ops.hrm_fa.flash_attn_paged(q, kp, kp, sl, 16, hm, True, 0, 0, None, None, None,
+                                          None, None)
     assert o.shape == q.shape and o.dtype == q.dtype
+    cs = torch.empty(64, 64, dtype=torch.float16, device="meta")
+    o = torch.ops.hrm_fa.flash_attn_paged(q, kp, kp, sl, 16, hm, True, 0, 0, None, None, None,
+                                          cs, cs)
+    assert o.shape == q.shape
     o2 = torch.ops.hrm_fa.flash_attn(q, q, q, True, 0, 0, None, None)
     assert o2.shape == q.shape
     kn = torch.empty(2, 2, 1, 128, dtype=torch.float16, device="meta")
-    assert torch.ops.hrm_fa.paged_kv_append(kp, kp, kn, kn, 0, None, 16, None) is None
+    assert torch.ops.hrm_fa.paged_kv_append(kp, kp, kn, kn, 0, None, 16, None, None, None) is None
+    assert torch.ops.hrm_fa.paged_kv_append(kp, kp, kn, kn, 0, None, 16, None, cs, cs) is None
 
 
 def test_product_path_does_not_import_the_oracle():
@@ -235,3 +253,16 @@ def test_product_path_does_not_import_the_oracle():
             if f.endswith(".py"):
                 src = open(os.path.join(root, f)).read()
                 assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", src, re.M), f
+
+
+@pytest.mark.parametrize("rope,msg", [
+    ((_f16(8, 64),), "rope must be"),
+    ((_f16(8, 32), _f16(8, 32)), r"cos/sin \[L, D/2\]"),
+    ((_f16(8, 64), _f16(9, 64)), r"cos/sin \[L, D/2\]"),
+    ((torch.zeros(8, 64), torch.zeros(8, 64)), "fp16 required"),
+    ((_f16(64, 8).t(), _f16(64, 8).t()), "contiguous required"),
+])
+def test_rope_table_validation(rope, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        ops._check_rope(rope, 128, torch.device("cpu"), require_device=False)
+    assert ops._check_rope(None, 128, torch.device("cpu"), require_device=False) == (None, None)

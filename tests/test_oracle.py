@@ -272,3 +272,65 @@ def test_append_skips_out_of_range_and_block_table():
     po, _ = ora.append_f16(pool, pool, kn, kn, [1, 3], PS, block_table=bt)
     assert _bitexact(po[0, :, 3, 1], kn[0, :, 0]) and _bitexact(po[0, :, 1, 3], kn[1, :, 0])
     assert not po[0, :, 0].any()  # b1 tokens 1..2 fall on the unmapped page -> skipped
+
+
+# ------------------------------------------------------------- rotary ----
+
+def test_rope_tables_match_closed_form():
+    cos, sin = ora.rope_tables(300, 128)
+    half = 64
+    ang = np.arange(300)[:, None] * (10000.0 ** (-np.arange(half) / half))[None, :]
+    assert cos.shape == (300, 64) and cos.dtype == np.float16
+    assert np.allclose(cos.astype(np.float64), np.cos(ang), atol=1e-3, rtol=0)
+    assert np.allclose(sin.astype(np.float64), np.sin(ang), atol=1e-3, rtol=0)
+
+
+def test_rope_f16_bitexact_vs_torch_fp16_arithmetic():
+    """The oracle's numpy emulation equals torch's fp16 CPU ops on the same
+    half-split expression, bit for bit."""
+    g = torch.Generator().manual_seed(5)
+    for D in (64, 128):
+        cos, sin = ora.rope_tables(512, D)
+        x = (torch.randn(2, 3, 40, D, generator=g) * 4).to(torch.float16)
+        pos = torch.randint(0, 512, (40,), generator=g)
+        c = torch.from_numpy(cos)[pos].view(1, 1, 40, D // 2)
+        s = torch.from_numpy(sin)[pos].view(1, 1, 40, D // 2)
+        x1, x2 = x[..., :D // 2], x[..., D // 2:]
+        want = torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], dim=-1).numpy()
+        got = ora.rope_f16(x, cos, sin, pos.numpy())
+        assert got.dtype == np.float16 and np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_rope_f16_invariants():
+    cos, sin = ora.rope_tables(4096, 128)
+    g = np.random.default_rng(3)
+    x = g.standard_normal((1, 2, 8, 128)).astype(np.float16)
+    # position 0: cos = 1, sin = 0 -> identity
+    assert np.array_equal(ora.rope_f16(x, cos, sin, np.zeros(8, np.int64)), x)
+    # rotation keeps the norm of every (x1_j, x2_j) pair (to fp16 rounding)
+    pos = g.integers(0, 4096, 8)
+    y = ora.rope_f16(x, cos, sin, pos).astype(np.float64)
+    xn = np.hypot(x[..., :64].astype(np.float64), x[..., 64:].astype(np.float64))
+    yn = np.hypot(y[..., :64], y[..., 64:])
+    assert np.allclose(xn, yn, atol=2e-2, rtol=4e-3)
+    # rotating by p1 then p2 equals rotating by p1 + p2 (angles add)
+    p1, p2 = g.integers(0, 2000, 8), g.integers(0, 2000, 8)
+    a = ora.rope_f16(ora.rope_f16(x, cos, sin, p1), cos, sin, p2).astype(np.float64)
+    b = ora.rope_f16(x, cos, sin, p1 + p2).astype(np.float64)
+    assert np.allclose(a, b, atol=3e-2, rtol=1e-2)
+
+
+def test_rope_planted_sign_error_is_caught():
+    cos, sin = ora.rope_tables(4096, 64)
+    g = np.random.default_rng(4)
+    x = g.standard_normal((1, 1, 16, 64)).astype(np.float16)
+    p1, p2 = g.integers(1, 2000, 16), g.integers(1, 2000, 16)
+
+    def wrong(v, pos):  # y1 = x1*c + x2*s (sign flipped)
+        c, s = cos[pos].astype(np.float32), sin[pos].astype(np.float32)
+        v1, v2 = v[..., :32].astype(np.float32), v[..., 32:].astype(np.float32)
+        return np.concatenate([(v1 * c + v2 * s), (v1 * s + v2 * c)], -1).astype(np.float16)
+
+    a = wrong(wrong(x, p1), p2).astype(np.float64)
+    b = wrong(x, p1 + p2).astype(np.float64)
+    assert not np.allclose(a, b, atol=3e-2, rtol=1e-2)
