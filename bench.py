@@ -35,7 +35,8 @@ import torch
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
-from hrm_flashrenderer_amd import flash_attn, flash_attn_paged, paged_kv_append, workloads  # noqa: E402
+from hrm_flashrenderer_amd import (build_rope_cache, flash_attn, flash_attn_paged,  # noqa: E402
+                                   paged_kv_append, workloads)
 
 METRIC = "decode attn HBM GB/s + prefill TFLOP/s (fp16) on 1 MI355X; % of roofline"
 PEAK_HBM_GBS = 8000.0
@@ -126,9 +127,11 @@ def bench_prefill(w, steps, warmup, traffic_key, traffic):
     }
 
 
-def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None):
+def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None):
     """Decode (+ append when the workload has new tokens). `rotate` is a second
-    workload with its own pool, alternated per step to defeat the 256 MB MALL."""
+    workload with its own pool, alternated per step to defeat the 256 MB MALL.
+    `rope=(cos, sin)`: the fused rotary variant (keys rotated by the append, the
+    query by the decode kernel)."""
     nbytes = workloads.decode_bytes(w)
     abytes = workloads.append_bytes(w) if w.k_new is not None else 0.0
     pools = [w] + ([rotate] if rotate is not None else [])
@@ -142,11 +145,12 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None):
             ev[0].record(stream)
         if x.k_new is not None:
             paged_kv_append(x.k_pool, x.v_pool, x.k_new, x.v_new, x.append_pos, 16,
-                            block_table=x.block_table)
+                            block_table=x.block_table, rope=rope)
         if ev:
             ev[1].record(stream)
         flash_attn_paged(x.q, x.k_pool, x.v_pool, x.seqlen, 16, x.head_map, False,
-                         block_table=x.block_table)
+                         x.append_pos if rope is not None else 0,
+                         block_table=x.block_table, rope=rope)
         if ev:
             ev[2].record(stream)
 
@@ -316,10 +320,14 @@ def main():
         w4 = workloads.cfg4(dev)
         extra["decode_cfg4"] = bench_decode(w4, K, W, "decode_cfg4", traffic)
         log(f"cfg4: decode {extra['decode_cfg4']['roofline']['achieved']} GB/s")
+        rope = build_rope_cache(max(w4.lengths) + 1, w4.D, device=dev)
+        extra["decode_cfg4_rope"] = bench_decode(w4, K, W, "decode_cfg4", traffic, rope=rope)
+        log(f"cfg4 with fused rotary embedding: decode "
+            f"{extra['decode_cfg4_rope']['roofline']['achieved']} GB/s")
         if not args.no_cpu_baseline:
             cpu["cfg4"] = cpu_baseline_paged(w4, "bytes")
             log(f"cfg4 cpu: {cpu['cfg4']}")
-        del w4
+        del w4, rope
     if "3" in cfgs:
         log("cfg3: building workload (two pools)")
         w3 = workloads.cfg3(dev)

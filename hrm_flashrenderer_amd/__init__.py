@@ -6,5 +6,7 @@ paged K/V cache (the caller-side cache of engine/llama_tp.py:21-107).
 """
 from .ops import flash_attn, flash_attn_paged, paged_kv_append
 from .kv_cache import PagedKVCache
+from .rope import build_rope_cache
 
-__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append", "PagedKVCache"]
+__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append", "PagedKVCache",
+           "build_rope_cache"]

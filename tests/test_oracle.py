@@ -334,3 +334,18 @@ def test_rope_planted_sign_error_is_caught():
     a = wrong(wrong(x, p1), p2).astype(np.float64)
     b = wrong(x, p1 + p2).astype(np.float64)
     assert not np.allclose(a, b, atol=3e-2, rtol=1e-2)
+
+
+def test_package_rope_tables_match_the_oracle_tables():
+    """hrm_flashrenderer_amd.build_rope_cache (the product's table builder)
+    against the oracle's restatement of engine/rope.py:6-13 (fp16 rounding of
+    the same fp32 angles; at most one fp16 ulp apart where cos/sin differ in
+    the last bit of their fp32 evaluation)."""
+    from hrm_flashrenderer_amd.rope import build_rope_cache
+    for D in (64, 128):
+        c, s = build_rope_cache(1000, D, device="cpu")
+        oc, os_ = ora.rope_tables(1000, D)
+        assert c.shape == (1000, D // 2) and c.dtype == torch.float16
+        dc = np.abs(c.numpy().astype(np.float64) - oc.astype(np.float64))
+        ds = np.abs(s.numpy().astype(np.float64) - os_.astype(np.float64))
+        assert dc.max() <= 2 ** -11 and ds.max() <= 2 ** -11
