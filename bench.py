@@ -87,6 +87,17 @@ def timed(step, steps, warmup, marks=1):
     return wall, segs
 
 
+def dist(durs):
+    """Summary of per-step kernel times in ms: mean, median, p10, p90, min, max."""
+    v = sorted(durs)
+
+    def q(f):
+        return v[min(len(v) - 1, max(0, int(round(f * (len(v) - 1)))))]
+    return {"mean": round(statistics.fmean(v), 4), "median": round(statistics.median(v), 4),
+            "p10": round(q(0.1), 4), "p90": round(q(0.9), 4), "min": round(v[0], 4),
+            "max": round(v[-1], 4)}
+
+
 def roofline(bound, work, mean_ms, traffic=None):
     if bound == "hbm":
         achieved = work / (mean_ms * 1e-3) / 1e9
@@ -119,8 +130,7 @@ def bench_prefill(w, steps, warmup, traffic_key, traffic):
     return {
         "value": round(flops * steps / wall / 1e12, 2), "unit": "TFLOP/s",
         "ms_per_step": round(wall / steps * 1e3, 4),
-        "kernel_ms": {"mean": round(mean_ms, 4), "median": round(statistics.median(durs), 4),
-                      "min": round(min(durs), 4), "max": round(max(durs), 4)},
+        "kernel_ms": dist(durs),
         "flops_per_step": flops,
         "roofline": roofline("mfma", flops, mean_ms, traffic.get(traffic_key)),
         "workload": workloads.sample_meta(w),
@@ -163,8 +173,7 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
         round((nbytes + abytes) * steps / wall / 1e9, 2),
         "unit": "GB/s",
         "ms_per_step": round(wall / steps * 1e3, 4),
-        "decode_kernel_ms": {"mean": round(mean_dec, 4), "median": round(statistics.median(dec), 4),
-                             "min": round(min(dec), 4), "max": round(max(dec), 4)},
+        "decode_kernel_ms": dist(dec),
         "decode_bytes_per_step": nbytes,
         "roofline": roofline("hbm", nbytes, mean_dec, traffic.get(traffic_key)),
         "cache_defeat": "two pools alternated" if rotate is not None else
@@ -173,7 +182,7 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
     }
     if abytes:
         mean_app = statistics.fmean(app)
-        out["append_kernel_ms"] = {"mean": round(mean_app, 4), "median": round(statistics.median(app), 4)}
+        out["append_kernel_ms"] = dist(app)
         out["append"] = roofline("hbm", abytes, mean_app, traffic.get("append"))
         out["append_bytes_per_step"] = abytes
         out["end_to_end_ms"] = round(statistics.fmean([a + d for a, d in zip(app, dec)]), 4)
@@ -204,11 +213,14 @@ def bench_cfg1(steps, warmup, dev):
 
 # ------------------------------------------------------------ CPU baseline ---
 
-def cpu_baseline_paged(w, kind, budget_s=8.0):
+def cpu_baseline_paged(w, kind, budget_s=10.0):
     """Time the oracle's restatement of the reference CPU path on this host.
 
-    The sample is a deterministic subset of sequences (and heads) chosen to fit
-    the budget, scaled to the same algorithmic unit as the GPU number."""
+    The sample is a deterministic prefix of the workload's (sequence, head)
+    pairs, sequence by sequence, sized from a timed probe so that the timed
+    run takes about `budget_s`; the rate is the sample's algorithmic work (the
+    same unit as the GPU figure) over its time. Attention only: the append
+    of the decode step is a copy of B rows."""
     from oracle import attention as ora
 
     threads = torch.get_num_threads()
@@ -218,53 +230,60 @@ def cpu_baseline_paged(w, kind, budget_s=8.0):
     sl = w.seqlen.cpu()
     hm = w.head_map.cpu()
     qo = w.q_offsets.cpu() if w.q_offsets is not None else 0
-    # probe one head of the first sequence to size the sample
-    t0 = time.perf_counter()
-    ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
-                             batches=[0], heads=[0])
-    per_head0 = max(time.perf_counter() - t0, 1e-4)
-    est_total = per_head0 * w.Hq * sum(w.lengths) / max(w.lengths[0], 1)
-    if kind == "flops":
-        est_total *= max(1.0, w.M / 64)
-    frac = min(1.0, budget_s / max(est_total, 1e-6))
-    nb = max(1, min(w.B, int(round(w.B * frac))))
-    batches = list(range(nb))
-    heads = None
-    if nb == 1 and frac * w.B < 1.0:
-        nh = max(1, min(w.Hq, int(w.Hq * frac * w.B)))
-        heads = list(range(nh))
-    if w.k_new is not None:
-        kc, vc = kp.clone(), vp.clone()
-        kn, vn, ap = w.k_new.cpu(), w.v_new.cpu(), w.append_pos.cpu()
-    t0 = time.perf_counter()
-    if w.k_new is not None:
-        ora.cpu_paged_kv_append(kc, vc, kn, vn, ap, 16, block_table=bt)
-    ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
-                             batches=batches, heads=heads)
-    dt = time.perf_counter() - t0
-    nh = w.Hq if heads is None else len(heads)
-    sub_pairs = 0
-    sub_tokens = 0
-    for b in batches:
+
+    def pairs_of(b):
         n = w.lengths[b]
-        sub_tokens += n
-        if w.causal:
-            off = w.q_offsets_host[b] if w.q_offsets_host else 0
-            sub_pairs += sum(max(0, min(n, off + i + 1)) for i in range(w.M))
-        else:
-            sub_pairs += w.M * n
+        if not w.causal:
+            return w.M * n
+        off = w.q_offsets_host[b] if w.q_offsets_host else 0
+        return sum(max(0, min(n, off + i + 1)) for i in range(w.M))
+
+    def run(batches, heads):
+        ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
+                                 batches=batches, heads=heads)
+
+    run([0], [0])                      # warm-up
+    t0 = time.perf_counter()
+    run([0], [0])
+    per_pair = max(time.perf_counter() - t0, 1e-5) / max(pairs_of(0), 1)
+    # a (sequence, head) costs about per_pair * pairs_of(b); take whole sequences
+    # while they fit the budget, then a prefix of the next one's heads
+    plan, spent = [], 0.0
+    for b in range(w.B):
+        head_cost = per_pair * max(pairs_of(b), 1)
+        if spent + head_cost * w.Hq <= budget_s:
+            plan.append((b, w.Hq))
+            spent += head_cost * w.Hq
+            continue
+        nh = int((budget_s - spent) / head_cost)
+        if nh >= 1:
+            plan.append((b, nh))
+        break
+    if not plan:
+        plan = [(0, 1)]
+    full = [b for b, nh in plan if nh == w.Hq]
+    part = [(b, nh) for b, nh in plan if nh < w.Hq]
+    t0 = time.perf_counter()
+    if full:
+        run(full, None)
+    for b, nh in part:
+        run([b], list(range(nh)))
+    dt = time.perf_counter() - t0
     if kind == "flops":
-        value = 4.0 * w.D * sub_pairs * nh / dt / 1e12
-        unit = "TFLOP/s"
+        work = sum(4.0 * w.D * pairs_of(b) * nh for b, nh in plan)
+        value, unit = work / dt / 1e12, "TFLOP/s"
     else:
-        sub_bytes = sub_tokens * w.Hk * w.D * 2 * 2 * nh / w.Hq + 2 * len(batches) * nh * w.M * w.D * 2
-        value = sub_bytes / dt / 1e9
-        unit = "GB/s"
-    sample = f"sequences {batches[0]}..{batches[-1]} of {w.B}"
-    sample += f", heads 0..{nh - 1} of {w.Hq}" if heads is not None else f", all {w.Hq} heads"
-    sample += f"; {dt:.2f} s on the host"
+        work = sum(w.lengths[b] * w.Hk * w.D * 2 * 2 * nh / w.Hq + 2 * nh * w.M * w.D * 2
+                   for b, nh in plan)
+        value, unit = work / dt / 1e9, "GB/s"
+    heads_done = sum(nh for _, nh in plan)
+    sample = (f"{heads_done} of {w.B * w.Hq} (sequence, head) pairs: sequences "
+              f"{plan[0][0]}..{plan[-1][0]} of {w.B}"
+              + (f" (the last with heads 0..{part[-1][1] - 1})" if part else "")
+              + f"; {dt:.2f} s on the host")
     return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port",
-            "sample": sample, "cpu": cpu_info(), "torch": torch.__version__}
+            "sample": sample, "extrapolated": heads_done < w.B * w.Hq,
+            "cpu": cpu_info(), "torch": torch.__version__}
 
 
 # -------------------------------------------------------------------- main ---
@@ -272,7 +291,7 @@ def cpu_baseline_paged(w, kind, budget_s=8.0):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="2,4,3,5,1")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -344,7 +363,7 @@ def main():
                                                       "prefill_cfg5", traffic)
         log(f"cfg5: {extra['chunked_prefill_cfg5']['value']} TFLOP/s")
         if not args.no_cpu_baseline:
-            cpu["cfg5"] = cpu_baseline_paged(w5, "flops", budget_s=6.0)
+            cpu["cfg5"] = cpu_baseline_paged(w5, "flops")
         del w5
     if "1" in cfgs:
         extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
