@@ -198,7 +198,8 @@ class PagedKVCache:
         raise ValueError("positions must be None, an int, [T] or [B, T]")
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor,
-               positions: PositionsLike = None, *, rope=None) -> None:
+               positions: PositionsLike = None, *, rope=None,
+               valid: Optional[Sequence[int]] = None) -> None:
         """Write k_new / v_new `[B, Hk, T, D]` at positions start_b .. start_b+T-1.
 
         `positions`: None (append at each sequence's current length), an int
@@ -207,6 +208,15 @@ class PagedKVCache:
         row consecutive). One kernel launch in every case. `rope=(cos, sin)`
         rotates the keys at their positions in the same launch (the
         reference's apply_rope on K, engine/llama_tp.py:183).
+
+        `valid` (host ints, one per sequence, each <= T): only the first
+        valid[b] tokens of sequence b are real (a ragged chunk padded to T);
+        its length becomes max(length, start_b + valid[b]) when valid[b] > 0
+        and stays put when it is 0. Pages are mapped for the real tokens only;
+        a padding token lands beyond the length in one of the sequence's own
+        pages or is skipped by the kernel (unmapped page). Padding must not
+        cover live tokens: a sequence whose length exceeds start_b + valid[b]
+        with valid[b] < T is rejected.
         """
         B, Hk, T, D = k_new.shape
         if B != self.bsz or Hk != self.kv_heads or D != self.head_dim:
@@ -214,9 +224,19 @@ class PagedKVCache:
         starts = self._starts(positions, T)
         if any(s < 0 for s in starts):
             raise ValueError("positions must be non-negative")
+        if valid is not None:
+            valid = [int(x) for x in valid]
+            if len(valid) != B or any(x < 0 or x > T for x in valid):
+                raise ValueError("valid must hold B counts in [0, T]")
+            for b, (st, n) in enumerate(zip(starts, valid)):
+                if n < T and self.lengths[b] > st + n:
+                    raise ValueError(f"padding tokens of sequence {b} would overwrite "
+                                     f"positions below its length {self.lengths[b]}")
         if T == 0:
             return
-        self._reserve_many([(b, -(-(s + T) // self.page_size)) for b, s in enumerate(starts)])
+        counts = valid if valid is not None else [T] * B
+        self._reserve_many([(b, -(-(s + n) // self.page_size)) for b, (s, n)
+                            in enumerate(zip(starts, counts)) if n > 0])
         uniform = len(set(starts)) == 1
         if uniform:
             start_arg: Union[int, torch.Tensor] = starts[0]
@@ -226,15 +246,20 @@ class PagedKVCache:
             start_arg = torch.tensor(starts, dtype=torch.int32).to(self.device, non_blocking=True)
         paged_kv_append(self.k_pages, self.v_pages, k_new.contiguous(), v_new.contiguous(),
                         start_arg, self.page_size, block_table=self._block_table, rope=rope)
-        # seqlen = max(seqlen, start + T), in stream order after the kernel
-        if uniform:
+        # seqlen = max(seqlen, start + count), in stream order after the kernel
+        if valid is not None:
+            ends = [st + n if n > 0 else 0 for st, n in zip(starts, counts)]
+            ends_dev = torch.tensor(ends, dtype=torch.int32).to(self.device, non_blocking=True)
+            torch.maximum(self.seqlen, ends_dev, out=self.seqlen)
+        elif uniform:
             self.seqlen.clamp_(min=starts[0] + T)
         elif positions is None:
             self.seqlen.add_(T)
         else:
             torch.maximum(self.seqlen, start_arg + T, out=self.seqlen)
-        for b, st in enumerate(starts):
-            self.lengths[b] = max(self.lengths[b], st + T)
+        for b, (st, n) in enumerate(zip(starts, counts)):
+            if n > 0:
+                self.lengths[b] = max(self.lengths[b], st + n)
         self.cur_len = max(self.lengths)
 
     def _set_lengths(self, new: dict, shrink: bool = False) -> None:
@@ -252,3 +277,23 @@ class PagedKVCache:
         return flash_attn_paged(q, self.k_pages, self.v_pages, self.seqlen, self.page_size,
                                 head_map, causal, q_offset, 0, block_table=self._block_table,
                                 rope=rope)
+
+
+def chunked_prefill_plan(prompt_lengths: Sequence[int], chunk_tokens: int) -> List[Tuple[int, List[int]]]:
+    """Chunks of a chunked prefill over prompts of different lengths.
+
+    The reference's generate loop (engine/llama_tp.py:339-354) prefills a batch
+    of equal-length prompts in chunks of `prefill_chunk_size` tokens at one
+    shared position. With ragged prompts, chunk c still starts every sequence
+    at position c * chunk_tokens (a scalar q_offset), and `valid[b]` says how
+    many of its tokens belong to prompt b. Pass it to `PagedKVCache.append`;
+    rows beyond `valid[b]` of the chunk's attention output are padding.
+    Returns [(start, valid), ...] for as many chunks as the longest prompt needs.
+    """
+    if chunk_tokens <= 0:
+        raise ValueError("chunk_tokens must be positive")
+    longest = max((int(n) for n in prompt_lengths), default=0)
+    plan = []
+    for start in range(0, longest, chunk_tokens):
+        plan.append((start, [max(0, min(chunk_tokens, int(n) - start)) for n in prompt_lengths]))
+    return plan

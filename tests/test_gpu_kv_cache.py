@@ -4,9 +4,12 @@ every sequence's keys and values (bit-exact K/V, tolerance bar on outputs)."""
 import pytest
 import torch
 
-from hrm_flashrenderer_amd.kv_cache import PagedKVCache
+import numpy as np
+
+from hrm_flashrenderer_amd.kv_cache import PagedKVCache, chunked_prefill_plan
+from hrm_flashrenderer_amd.rope import build_rope_cache
 from oracle import attention as ora
-from paged_ref import assert_close, gather_seq, seeded
+from paged_ref import assert_close, gather_seq, poison_dead_slots, seeded
 
 pytestmark = pytest.mark.gpu
 
@@ -135,3 +138,71 @@ def test_llama_tp_attention_pattern(gpu):
             shadow.write(b, cur, k[b].cpu(), v[b].cpu())
         _check_attention(cache, shadow, q, hm, T > 1, cur, f"step {step}")
         cur += T
+
+
+@pytest.mark.parametrize("page_size,chunk,use_rope", [(16, 128, False), (128, 100, True),
+                                                      (64, 256, False)])
+def test_chunked_prefill_of_ragged_prompts(gpu, page_size, chunk, use_rope):
+    """Prompts of different lengths (one empty) prefilled chunk by chunk at a
+    shared position (q_offset = chunk start), each chunk padded to a common T
+    with `valid` per sequence; dead slots are NaN-poisoned before every
+    attention call, then one ragged decode step follows."""
+    B, Hq, Hk, D = 4, 8, 2, 128
+    prompts = [300, 77, 0, 256]
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    cache = PagedKVCache(B, Hk, D, page_size=page_size, init_pages=1, device=gpu)
+    L = 512
+    rope = build_rope_cache(L, D, device=gpu) if use_rope else None
+    kf = [seeded((Hk, n, D), 100 + b).cpu() for b, n in enumerate(prompts)]
+    vf = [seeded((Hk, n, D), 200 + b).cpu() for b, n in enumerate(prompts)]
+    qf = [seeded((Hq, n, D), 300 + b).cpu() for b, n in enumerate(prompts)]
+
+    def rot(x, pos):
+        if rope is None:
+            return x
+        return torch.from_numpy(ora.rope_f16(x, rope[0].cpu(), rope[1].cpu(), pos))
+
+    plan = chunked_prefill_plan(prompts, chunk)
+    assert len(plan) == -(-max(prompts) // chunk)
+    for ci, (start, valid) in enumerate(plan):
+        pad = seeded((3, B, max(Hq, Hk), chunk, D), 900 + ci).cpu()  # padding tokens
+        k = pad[0, :, :Hk].clone()
+        v = pad[1, :, :Hk].clone()
+        q = pad[2].clone()
+        for b, n in enumerate(valid):
+            k[b, :, :n] = kf[b][:, start:start + n]
+            v[b, :, :n] = vf[b][:, start:start + n]
+            q[b, :, :n] = qf[b][:, start:start + n]
+        before = list(cache.lengths)
+        cache.append(k.to(gpu), v.to(gpu), start, valid=valid, rope=rope)
+        want = [max(before[b], start + n) if n else before[b] for b, n in enumerate(valid)]
+        assert cache.lengths == want and cache.seqlen.cpu().tolist() == want
+        poison_dead_slots(cache.k_pages, cache.v_pages, cache.block_table, cache.lengths,
+                          page_size)
+        out = cache.attention(q.to(gpu), hm, True, start, rope=rope).cpu()
+        for b, n in enumerate(valid):
+            if n == 0:
+                continue
+            end = start + n
+            ref = ora.attention_f64(rot(q[b:b + 1, :, :n], np.arange(start, end)),
+                                    rot(kf[b][None, :, :end], np.arange(end)),
+                                    vf[b][None, :, :end], True, start, 0,
+                                    head_map=hm.cpu().tolist())
+            assert_close(out[b:b + 1, :, :n], ref, f"chunk {ci} b={b}")
+    assert cache.lengths == prompts
+    # the pool holds exactly the (rotated) prompts
+    kc, vc, bt = cache.k_pages.cpu(), cache.v_pages.cpu(), cache.block_table.cpu()
+    for b, n in enumerate(prompts):
+        assert torch.equal(gather_seq(kc, bt[b], n, page_size), rot(kf[b], np.arange(n))), b
+        assert torch.equal(gather_seq(vc, bt[b], n, page_size), vf[b]), b
+    # one decode step at the ragged lengths (device-side starts)
+    kd, vd, qd = seeded((B, Hk, 1, D), 51), seeded((B, Hk, 1, D), 52), seeded((B, Hq, 1, D), 53)
+    cache.append(kd, vd, rope=rope)
+    qo = torch.tensor(prompts, dtype=torch.int32, device=gpu)
+    out = cache.attention(qd, hm, True, qo, rope=rope).cpu()
+    for b, n in enumerate(prompts):
+        kk = torch.cat([rot(kf[b], np.arange(n)), rot(kd[b].cpu(), np.arange(n, n + 1))], 1)
+        vv = torch.cat([vf[b], vd[b].cpu()], 1)
+        ref = ora.attention_f64(rot(qd[b:b + 1].cpu(), np.arange(n, n + 1)), kk[None], vv[None],
+                                True, n, 0, head_map=hm.cpu().tolist())
+        assert_close(out[b:b + 1], ref, f"decode b={b}")

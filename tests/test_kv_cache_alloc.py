@@ -87,3 +87,26 @@ def test_append_on_a_cpu_cache_raises_instead_of_computing():
     k = torch.zeros(3, 2, 3, 64, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="CUDA required"):
         c.append(k, k)
+
+
+def test_chunked_prefill_plan():
+    from hrm_flashrenderer_amd.kv_cache import chunked_prefill_plan
+    assert chunked_prefill_plan([700, 130, 0, 256], 256) == [
+        (0, [256, 130, 0, 256]), (256, [256, 0, 0, 0]), (512, [188, 0, 0, 0])]
+    assert chunked_prefill_plan([], 64) == []
+    assert chunked_prefill_plan([5], 64) == [(0, [5])]
+    with pytest.raises(ValueError):
+        chunked_prefill_plan([5], 0)
+
+
+def test_valid_counts_are_validated():
+    c = _cache()
+    k = torch.zeros(3, 2, 4, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="valid"):
+        c.append(k, k, 0, valid=[4, 5, 0])
+    with pytest.raises(ValueError, match="valid"):
+        c.append(k, k, 0, valid=[1, 2])
+    c._set_lengths({0: 10})
+    k8 = torch.zeros(3, 2, 8, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="overwrite"):
+        c.append(k8, k8, 0, valid=[5, 8, 8])
