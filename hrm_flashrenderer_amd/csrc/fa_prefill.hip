@@ -339,7 +339,9 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 //    the 8 XCDs, so slot L runs item (L % 8) * per_xcd + L / 8 of a list
 //    ordered by (sequence, KV-head group, q tile descending, head in group):
 //    all q tiles and heads that share one KV head run on one XCD's L2, longest
-//    rows first.
+//    rows first. When every XCD owns whole (sequence, KV group) pairs, the
+//    32-key kernel orders each XCD's items by q tile descending across its
+//    pairs (longest first over the whole XCD, which shortens the tail).
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
@@ -792,11 +794,24 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const int item = (slot & 7) * per_xcd + (slot >> 3);
   if (item >= total) return;
   const int per_pair = ntq * group;
-  const int pair = item / per_pair;
-  const int rem = item - pair * per_pair;
-  const int qt = ntq - 1 - rem / group;
+  int pair = item / per_pair;
+  int rem = item - pair * per_pair;
+  int qt = ntq - 1 - rem / group;
+  int head = rem % group;
+  if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
+    // Each XCD owns whole (sequence, KV group) pairs: run its items longest
+    // q tile first across all of them (the greedy longest-first order evens
+    // out the finishing times of the XCD's workgroup slots).
+    const int kp = per_xcd / per_pair;
+    const int l = slot >> 3;
+    const int band = kp * group;
+    const int r = l / band, w = l - r * band;
+    pair = (slot & 7) * kp + w / group;
+    qt = ntq - 1 - r;
+    head = w % group;
+  }
   const int ngroups = p.Hq / group;
-  const int hq = (pair % ngroups) * group + rem % group;
+  const int hq = (pair % ngroups) * group + head;
   const int b = pair / ngroups;
 
   const int tid = threadIdx.x;
