@@ -37,6 +37,9 @@ SYMBOLS = (
       _P, _SZ, _P, _P, _I, _P]),
     ("fa_paged_kv_append_rope", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P, _P, _I, _P]),
+    ("fa_decode_token_major", _I,
+     [_P, _P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P, _SZ, _P]),
+    ("fa_decode_token_major_workspace_bytes", _SZ, [_I, _I, _I, _I]),
     ("fa_last_error", ctypes.c_char_p, []),
     ("fa_abi_version", _I, []),
 )

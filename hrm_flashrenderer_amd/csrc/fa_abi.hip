@@ -54,6 +54,7 @@ fa::KVMap paged_map(const int32_t* block_table, int max_blocks, int NB, int Hk, 
   m.stride_page = (int64_t)PS * D;
   m.stride_hk = (int64_t)P * m.stride_page;
   m.stride_nb = (int64_t)Hk * m.stride_hk;
+  m.stride_tok = D;
   m.max_blocks = block_table ? max_blocks : P;
   m.P = P;
   const int64_t phys = (int64_t)NB * P;
@@ -116,6 +117,7 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
   p.kv.stride_hk = (int64_t)N * D;
   p.kv.stride_nb = (int64_t)Hk * p.kv.stride_hk;
   p.kv.stride_page = 0;
+  p.kv.stride_tok = D;
   p.kv.max_blocks = 0;
   p.kv.P = 0;
   p.kv.num_phys = 0;
@@ -268,6 +270,69 @@ int fa_paged_kv_append_rope(void* k_pages, void* v_pages, const void* k_new, con
     return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
   return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, start_pos,
                    start_positions, block_table, max_blocks, rope_cos, rope_sin, rope_len, stream);
+}
+
+size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max) {
+  if (H <= 0 || KVH <= 0 || !head_dim_ok(Dh) || t_max < 0 || t_max >= INT_MAX) return 0;
+  if (!fa::use_decode_path(1, 1, H, KVH)) return 0;
+  return fa::plan_decode(1, H, 1, Dh, KVH, t_max + 1).ws_bytes;
+}
+
+int fa_decode_token_major(float* out, const float* q, const void* k_cache, const void* v_cache,
+                          int t, int H, int KVH, int Dh, float scale, const int32_t* head_map,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (H <= 0 || KVH <= 0) return fail(FA_ERR_INVALID, "H and KVH must be positive");
+  if (!head_dim_ok(Dh)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
+  if (t < 0 || t >= INT_MAX) return fail(FA_ERR_INVALID, "position t out of range");
+  if (!isfinite(scale)) return fail(FA_ERR_INVALID, "scale must be finite");
+  if (!fa::use_decode_path(1, 1, H, KVH))
+    return fail(FA_ERR_INVALID, "unsupported head counts H=%d KVH=%d", H, KVH);
+  if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr)
+    return fail(FA_ERR_INVALID, "null tensor pointer");
+
+  fa::AttnParams p = {};
+  p.q = q;
+  p.q_f32 = 1;
+  p.k = k_cache;
+  p.v = v_cache;
+  p.o = out;
+  p.o_f32 = 1;
+  p.seqlen = nullptr;  // all t + 1 rows
+  p.head_map = head_map;
+  p.head_mod = head_map == nullptr ? 1 : 0;
+  p.kv.block_table = nullptr;
+  p.kv.stride_nb = 0;
+  p.kv.stride_hk = Dh;
+  p.kv.stride_tok = (int64_t)KVH * Dh;
+  p.kv.stride_page = 0;
+  p.kv.max_blocks = 0;
+  p.kv.P = 0;
+  p.kv.num_phys = 0;
+  p.kv.PS = 1;
+  p.kv.ps_shift = 0;
+  p.kv.D = Dh;
+  p.kv.paged = 0;
+  p.B = 1;
+  p.Hq = H;
+  p.Hk = KVH;
+  p.M = 1;
+  p.N = t + 1;
+  p.group = H >= KVH ? H / KVH : 1;
+  p.causal = 0;
+  p.scale_log2 = scale * fa::kLog2e;
+
+  (void)hipGetLastError();
+  const fa::DecodePlan plan = fa::plan_decode(1, H, 1, Dh, KVH, p.N);
+  if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
+    return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+  char* ws = reinterpret_cast<char*>(workspace);
+  p.ws_o = reinterpret_cast<float*>(ws);
+  p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
+  p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
+  p.dec_wgs = fa::decode_launch_wgs(plan, Dh, false);  // strided rows: per-row loads
+  p.dec_rows = plan.rows;
+  return launch_status(fa::launch_decode(p, Dh, (hipStream_t)stream));
 }
 
 }  // extern "C"

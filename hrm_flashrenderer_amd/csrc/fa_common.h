@@ -23,7 +23,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Where the K/V rows of one (sequence, KV head) live.
 //
-// Contiguous K/V [B, Hk, N, D]: row j of (b, hk) is at ((b*Hk + hk)*N + j)*D.
+// Contiguous K/V [B, Hk, N, D]: row j of (b, hk) is at ((b*Hk + hk)*N + j)*D;
+// in general b*stride_nb + hk*stride_hk + j*stride_tok, which also covers the
+// token-major cache [N, Hk, D] (stride_hk = D, stride_tok = Hk*D).
 // Paged K/V [NB, Hk, P, PS, D]: logical page p = j / PS of sequence b maps to
 // a physical id phi (identity b*P + p, or block_table[b*max_blocks + p]), and
 // the row sits at (((phi/P)*Hk + hk)*P + phi%P)*PS*D + (j%PS)*D. The map follows
@@ -34,6 +36,7 @@ struct KVMap {
   int64_t stride_nb;           // Hk*P*PS*D (paged) ; Hk*N*D (contiguous)
   int64_t stride_hk;           // P*PS*D           ; N*D
   int64_t stride_page;         // PS*D             ; unused
+  int64_t stride_tok;          // unused           ; D (Hk*D token-major)
   int max_blocks;              // logical pages per sequence (P without table)
   int P;                       // pages per row of the pool
   int num_phys;                // NB*P: valid physical ids are [0, num_phys)
@@ -48,7 +51,7 @@ struct KVMap {
   // constant address space (s_load), and the physical id is split into
   // (pool row, page) only when the pool has more than one row.
   __device__ __forceinline__ int64_t row_offset(int b, int hk, int j) const {
-    if (!paged) return (int64_t)b * stride_nb + (int64_t)hk * stride_hk + (int64_t)j * D;
+    if (!paged) return (int64_t)b * stride_nb + (int64_t)hk * stride_hk + (int64_t)j * stride_tok;
     unsigned page, slot;
     if (ps_shift >= 0) {
       page = (unsigned)j >> ps_shift;
@@ -107,6 +110,11 @@ struct AttnParams {
   const f16* rope_cos;
   const f16* rope_sin;
   int rope_len;
+  // decode only: fp32 Q and O (converted on load / store) and, without a head
+  // map, the q-head -> KV-head map hq % Hk (instead of hq / group)
+  int q_f32;
+  int o_f32;
+  int head_mod;
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
@@ -119,7 +127,7 @@ struct AttnParams {
   }
   // K/V head of query head hq, or -1 if the head map points outside [0, Hk).
   __device__ __forceinline__ int kv_head(int hq) const {
-    if (head_map == nullptr) return hq / group;
+    if (head_map == nullptr) return head_mod ? hq % Hk : hq / group;
     int hk = head_map[hq];
     return (hk >= 0 && hk < Hk) ? hk : -1;
   }

@@ -299,7 +299,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       for (int kk = 0; kk < KSTEPS; ++kk) {
         if (row_ok) {
           const int64_t qoff = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 32 * kk + 8 * quarter;
-          qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
+          if (p.q_f32) {
+            const floatx4 lo = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.q) + qoff);
+            const floatx4 hi =
+                *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.q) + qoff + 4);
+            qreg[kk] = half8{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3],
+                             (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
+          } else {
+            qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
+          }
         } else {
           qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
@@ -554,8 +562,14 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = acc[k] * inv;
   }
+  if (p.o_f32) {
+    float* of = reinterpret_cast<float*>(p.o) + (int64_t)row * D;
 #pragma unroll
-  for (int k = 0; k < DPW; ++k) op[lane + 64 * k] = (f16)result[k];
+    for (int k = 0; k < DPW; ++k) of[lane + 64 * k] = result[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) op[lane + 64 * k] = (f16)result[k];
+  }
 }
 
 int env_int(const char* name, int fallback) {
@@ -628,7 +642,7 @@ hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
   const dim3 grid((unsigned)p.dec_wgs);
   const int rows = p.B * p.Hq * p.M;
   const dim3 cgrid((unsigned)((rows + 3) / 4));
-  const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
+  const bool aligned = p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D;
   const dim3 block(kDecodeThreads);
   if (D == 128) {
     if (aligned)

@@ -1105,7 +1105,7 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
       hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(64), 0, stream, p);
     return hipGetLastError();
   }
-  const bool aligned = !p.kv.paged || (p.kv.PS % 16) == 0;
+  const bool aligned = p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D;
   const int ntq = (p.M + kBM - 1) / kBM;
   if (!aligned) {
     const dim3 grid((unsigned)ntq, (unsigned)p.Hq, (unsigned)p.B);

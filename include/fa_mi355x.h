@@ -157,6 +157,27 @@ int fa_paged_kv_append_rope(void* k_pages, void* v_pages,
                             const void* rope_cos, const void* rope_sin, int rope_len,
                             void* stream);
 
+/*
+ * Single-sequence decode attention over a token-major fp16 KV cache: the
+ * cache layout, head mapping and fp32 input/output of the reference's INT8
+ * engine decode step (attn_decode, scripts/deepseek_native_engine.sh:562-604,
+ * launched at :1077 after kv_store at :1074), run on the paged-decode kernels:
+ *   out[h, :] = sum_{j <= t} softmax_j(scale * q[h, :] . K[j, kvh, :]) V[j, kvh, :]
+ *   kvh = head_map ? head_map[h] : h % KVH     (the engine's mapping, :568)
+ *   q, out           : fp32 [H, Dh]
+ *   k_cache, v_cache : fp16 [>= t + 1, KVH, Dh]; row j of KV head kvh at
+ *                      element j*KVH*Dh + kvh*Dh (the engine's Kc/Vc, :553-559)
+ * Q is rounded to fp16 for the matrix cores; scores, softmax and the output
+ * accumulate in fp32. A head_map entry outside [0, KVH) yields NaN rows.
+ * workspace: fa_decode_token_major_workspace_bytes(H, KVH, Dh, t_max) bytes
+ * for any t <= t_max (0 when the shape is unsupported).
+ */
+int fa_decode_token_major(float* out, const float* q, const void* k_cache, const void* v_cache,
+                          int t, int H, int KVH, int Dh, float scale, const int32_t* head_map,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* fa_last_error(void);
 

@@ -8,6 +8,8 @@ Contents
   1. fp64 closed form (numpy): the tolerance target of every GPU parity test
      (outputs within 2e-3 + 1e-2*|ref| of the exact softmax attention).
        attention_f64            O = softmax(Q K^T / sqrt(D) + mask) V
+       decode_token_major_f64   the INT8 engine's decode step over its
+                                token-major cache (deepseek_native_engine.sh:562-604)
   2. Page-map helpers (numpy): the reference's paged layout and the additive
      block-table indirection; the rotary embedding the fused kernels apply.
        gather_kv                pages -> contiguous [B, Hk, cap, D]
@@ -26,6 +28,11 @@ How each function is pinned (tests/test_oracle.py):
                     float64 with an explicit mask; invariants (one visible key
                     -> v, equal scores -> mean of V, shift invariance, key
                     permutation invariance, GQA == MHA with repeated K/V).
+  decode_token_major_f64
+                    == attention_f64 on the re-laid-out cache with head map
+                    h % KVH; == a per-key transcription of the engine's online
+                    recurrence (m, s, acc) on a tiny case; t = 0 gives v_0; a
+                    planted h // group head map fails.
   gather_kv         identity block table == reference flatten (ops.py:43-45);
                     a permuted pool gathered == the unpermuted original.
   append_f16        the reference's append known-answer test shape
@@ -112,6 +119,36 @@ def attention_f64(q: ArrayLike, k: ArrayLike, v: ArrayLike, causal: bool = True,
                 e = np.exp(s - mx)
                 p = e / e.sum(axis=1, keepdims=True)
             out[b, h] = p @ vn[b, hk, :n]
+    return out
+
+
+def decode_token_major_f64(q: ArrayLike, k_cache: ArrayLike, v_cache: ArrayLike, t: int,
+                           scale: Optional[float] = None,
+                           head_map: Optional[Sequence[int]] = None) -> np.ndarray:
+    """Decode attention of the reference's INT8 engine in float64.
+
+    attn_decode (scripts/deepseek_native_engine.sh:562-604): query head h
+    attends keys 0..t of KV head kvh = h % KVH (:568; or head_map[h]) in the
+    token-major fp16 cache written by kv_store (:553-559), row j of head kvh at
+    j*KVH*Dh + kvh*Dh; scale = 1/sqrt(Dh) as launched (:1077).
+    q [H, Dh]; k_cache, v_cache [T, KVH, Dh] with T > t. Returns [H, Dh].
+    """
+    qn = _np(q).astype(np.float64)
+    kn = _np(k_cache).astype(np.float64)
+    vn = _np(v_cache).astype(np.float64)
+    H, Dh = qn.shape
+    KVH = kn.shape[1]
+    sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
+    hmap = np.arange(H) % KVH if head_map is None else _np(head_map).astype(np.int64)
+    out = np.zeros((H, Dh), dtype=np.float64)
+    for h in range(H):
+        kvh = int(hmap[h])
+        if not (0 <= kvh < KVH):
+            out[h] = np.nan
+            continue
+        s = (kn[:t + 1, kvh] @ qn[h]) * sc
+        e = np.exp(s - s.max())
+        out[h] = (e / e.sum()) @ vn[:t + 1, kvh]
     return out
 
 

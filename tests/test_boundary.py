@@ -30,7 +30,8 @@ def declared_functions():
 
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
-        "fa_abi_version", "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd",
+        "fa_abi_version", "fa_decode_token_major", "fa_decode_token_major_workspace_bytes",
+        "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd",
         "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
         "fa_paged_kv_append_rope", "fa_paged_workspace_bytes"])
 
@@ -84,6 +85,21 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
         P, P, P, P, 2, 4, 3, 24, 2, 4, 16, 0, None, None, 0, P, P, 64, None))
     assert rc == -1 and msg == "rotary append needs head_dim a multiple of 16"
+    # token-major decode (the INT8 engine's cache): shapes, scale, workspace
+    tm = lib.fa_decode_token_major
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 96, 0.1, None, P, 1 << 20, None))
+    assert rc == -1 and msg == "Supported head_dim: 64 or 128"
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 0, 8, 128, 0.1, None, P, 1 << 20, None))
+    assert rc == -1 and msg == "H and KVH must be positive"
+    rc, msg = _status_and_message(tm(P, P, P, P, -1, 40, 8, 128, 0.1, None, P, 1 << 20, None))
+    assert rc == -1 and msg == "position t out of range"
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, float("inf"), None, P, 1 << 20,
+                                     None))
+    assert rc == -1 and msg == "scale must be finite"
+    rc, msg = _status_and_message(tm(P, P, None, P, 5, 40, 8, 128, 0.1, None, P, 1 << 20, None))
+    assert rc == -1 and msg == "null tensor pointer"
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, 0.1, None, P, 16, None))
+    assert rc == -3 and msg.startswith("workspace of")
     # empty work returns OK without any launch
     assert lib.fa_flash_attn_fwd(P, P, P, P, 0, 0, 8, 8, 16, 16, 64, 1, 0, 0, None, None, None) == 0
     assert lib.fa_paged_kv_append(P, P, P, P, 2, 4, 0, 128, 2, 4, 16, 0, None, None, 0, None) == 0
@@ -103,6 +119,13 @@ def test_workspace_sizing_depends_on_sizes_only():
     # prefill-shaped calls need no workspace
     assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16) == 0
     assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16) == 0
+    # token-major decode: one sequence of t_max + 1 keys, rows = H
+    t_max = 4095  # 256 groups x 8 KV heads = 2048 units -> 256 workgroups
+    ws = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max)
+    slots = 8 + 256
+    assert ws == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 2 * 4
+    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100) < ws
+    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max) == 0
 
 
 def test_signatures_match_reference():

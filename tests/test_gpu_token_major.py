@@ -1,0 +1,71 @@
+"""Decode attention over the INT8 engine's token-major cache on the GPU
+(attn_decode, scripts/deepseek_native_engine.sh:562-604, through the C entry
+fa_decode_token_major): fp32 q, fp16 [T, KVH, Dh] caches, head map h % KVH by
+default, against the fp64 oracle at the fp32-softmax tolerance. Rows past t
+are NaN-poisoned, so a read beyond the attended keys shows up as NaN."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from hrm_flashrenderer_amd.token_major import decode_token_major, workspace_bytes
+from oracle import attention as ora
+from paged_ref import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(T, KVH, Dh, H, seed, gpu):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, Dh, generator=g, dtype=torch.float32)
+    k = torch.randn(T, KVH, Dh, generator=g).to(torch.float16)
+    v = torch.randn(T, KVH, Dh, generator=g).to(torch.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("H,KVH,Dh", [(40, 8, 128), (64, 8, 128), (32, 32, 64), (14, 2, 64)])
+@pytest.mark.parametrize("t", [0, 1, 15, 16, 17, 255, 1000, 4095])
+def test_token_major_decode_matches_oracle(gpu, H, KVH, Dh, t):
+    T = t + 9
+    q, k, v = _case(T, KVH, Dh, H, 1000 + t + H, gpu)
+    kd, vd = k.clone(), v.clone()
+    kd[t + 1:] = float("nan")
+    vd[t + 1:] = float("nan")
+    out = decode_token_major(q.to(gpu), kd.to(gpu), vd.to(gpu), t).cpu()
+    assert out.dtype == torch.float32 and out.shape == (H, Dh)
+    ref = ora.decode_token_major_f64(q, k, v, t)
+    assert_close(out, ref, f"H={H} KVH={KVH} Dh={Dh} t={t}")
+
+
+def test_token_major_decode_head_map_scale_and_workspace_reuse(gpu):
+    H, KVH, Dh, T = 40, 8, 128, 700
+    q, k, v = _case(T, KVH, Dh, H, 77, gpu)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    ws = torch.empty(workspace_bytes(H, KVH, Dh, T - 1), dtype=torch.uint8, device=gpu)
+    hm = [h // (H // KVH) for h in range(H)]  # the HF GQA mapping instead of h % KVH
+    hm_d = torch.tensor(hm, dtype=torch.int32, device=gpu)
+    for t, scale in ((T - 1, None), (300, 0.05), (5, 1.0 / math.sqrt(Dh))):
+        out = decode_token_major(qd, kd, vd, t, scale=scale, head_map=hm_d, workspace=ws).cpu()
+        ref = ora.decode_token_major_f64(q, k, v, t, scale=scale, head_map=hm)
+        assert_close(out, ref, f"head_map t={t} scale={scale}")
+    # out-of-range head map entries give NaN rows, the others stay exact
+    bad = hm_d.clone()
+    bad[3] = KVH
+    out = decode_token_major(qd, kd, vd, 100, head_map=bad, workspace=ws).cpu()
+    assert torch.isnan(out[3]).all()
+    ref = ora.decode_token_major_f64(q, k, v, 100, head_map=[h if i != 3 else 0 for i, h in enumerate(hm)])
+    keep = [i for i in range(H) if i != 3]
+    assert_close(out[keep], ref[keep], "head map with one bad entry")
+
+
+def test_token_major_decode_rejects_bad_calls(gpu):
+    q, k, v = _case(8, 2, 64, 4, 3, gpu)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    with pytest.raises(RuntimeError, match="outside the cache"):
+        decode_token_major(qd, kd, vd, 8)
+    with pytest.raises(RuntimeError, match="q must be fp32"):
+        decode_token_major(qd.half(), kd, vd, 3)
+    small = torch.empty(16, dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError, match="workspace of"):
+        decode_token_major(qd, kd, vd, 3, workspace=small)

@@ -349,3 +349,59 @@ def test_package_rope_tables_match_the_oracle_tables():
         dc = np.abs(c.numpy().astype(np.float64) - oc.astype(np.float64))
         ds = np.abs(s.numpy().astype(np.float64) - os_.astype(np.float64))
         assert dc.max() <= 2 ** -11 and ds.max() <= 2 ** -11
+
+
+# ---- the INT8 engine's token-major decode (deepseek_native_engine.sh:562-604) ----
+
+def _engine_cache(T, KVH, Dh, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, Dh, generator=g, dtype=torch.float32)
+    k = torch.randn(T, KVH, Dh, generator=g).to(torch.float16)
+    v = torch.randn(T, KVH, Dh, generator=g).to(torch.float16)
+    return q, k, v
+
+
+def test_token_major_decode_equals_closed_form_with_modulo_heads():
+    H, KVH, Dh, T, t = 10, 4, 16, 40, 23
+    q, k, v = _engine_cache(T, KVH, Dh, H, 5)
+    out = ora.decode_token_major_f64(q, k, v, t)
+    # the same attention through attention_f64: [1, KVH, t+1, Dh] and head map h % KVH
+    kk = k[:t + 1].permute(1, 0, 2)[None]
+    vv = v[:t + 1].permute(1, 0, 2)[None]
+    ref = ora.attention_f64(q[None, :, None, :], kk, vv, False,
+                            head_map=[h % KVH for h in range(H)])[0, :, 0]
+    assert np.allclose(out, ref, rtol=0, atol=1e-12)
+
+
+def test_token_major_decode_matches_the_engine_recurrence():
+    # per-key online softmax exactly as attn_decode updates (m, s, acc), :571-600
+    H, KVH, Dh, T, t = 6, 2, 8, 9, 6
+    q, k, v = _engine_cache(T, KVH, Dh, H, 6)
+    out = ora.decode_token_major_f64(q, k, v, t, scale=1 / math.sqrt(Dh))
+    for h in range(H):
+        kvh = h % KVH
+        m, s, acc = -1e30, 0.0, np.zeros(Dh)
+        for kpos in range(t + 1):
+            dot = float(np.dot(q[h].double().numpy(), k[kpos, kvh].double().numpy())) / math.sqrt(Dh)
+            new_m = max(m, dot)
+            e_old, e_new = math.exp(m - new_m), math.exp(dot - new_m)
+            acc = acc * e_old + v[kpos, kvh].double().numpy() * e_new
+            s = s * e_old + e_new
+            m = new_m
+        assert np.allclose(out[h], acc / max(s, 1e-10), rtol=0, atol=1e-12)
+
+
+def test_token_major_decode_invariants_and_planted_head_map():
+    H, KVH, Dh, T = 8, 2, 16, 12
+    q, k, v = _engine_cache(T, KVH, Dh, H, 7)
+    out0 = ora.decode_token_major_f64(q, k, v, 0)   # one visible key -> its value row
+    for h in range(H):
+        assert np.allclose(out0[h], v[0, h % KVH].double().numpy(), atol=1e-12)
+    out = ora.decode_token_major_f64(q, k, v, T - 1)
+    planted = ora.decode_token_major_f64(q, k, v, T - 1, head_map=[h // (H // KVH) for h in range(H)])
+    assert not np.allclose(out, planted, atol=1e-3)
+    # keys past t never matter
+    k2, v2 = k.clone(), v.clone()
+    k2[6:] = float("nan")
+    v2[6:] = float("nan")
+    assert np.array_equal(ora.decode_token_major_f64(q, k2, v2, 5), ora.decode_token_major_f64(q, k, v, 5))
