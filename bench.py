@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention path on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1,tm]
                     [--no-cpu-baseline]
 
 Prints ONE JSON line on stdout (diagnostics go to stderr). The headline
@@ -37,6 +37,8 @@ sys.path.insert(0, REPO)
 
 from hrm_flashrenderer_amd import (build_rope_cache, flash_attn, flash_attn_paged,  # noqa: E402
                                    paged_kv_append, workloads)
+from hrm_flashrenderer_amd.token_major import decode_token_major  # noqa: E402
+from hrm_flashrenderer_amd.token_major import workspace_bytes as token_major_workspace  # noqa: E402
 
 METRIC = "decode attn HBM GB/s + prefill TFLOP/s (fp16) on 1 MI355X; % of roofline"
 PEAK_HBM_GBS = 8000.0
@@ -211,6 +213,39 @@ def bench_cfg1(steps, warmup, dev):
     return res
 
 
+def bench_token_major(steps, warmup, dev, H=40, KVH=8, Dh=128, t=32767, sets=3):
+    """The INT8 engine's decode step (batch 1, token-major fp16 cache, fp32 q and
+    out) at the Qwen-32B head counts and a 32K context, rotating `sets` caches
+    (3 x 134 MB of K and V) so the step reads HBM, not the 256 MB MALL."""
+    g = torch.Generator().manual_seed(1006)
+    q = torch.randn(H, Dh, generator=g).to(dev)
+    caches = []
+    for _ in range(sets):
+        k = torch.randn(t + 1, KVH, Dh, generator=g).to(torch.float16).to(dev)
+        v = torch.randn(t + 1, KVH, Dh, generator=g).to(torch.float16).to(dev)
+        caches.append((k, v))
+    ws = torch.empty(token_major_workspace(H, KVH, Dh, t), dtype=torch.uint8, device=dev)
+    nbytes = (t + 1) * KVH * Dh * 2 * 2 + 2 * H * Dh * 4
+    stream = torch.cuda.current_stream()
+    it = [0]
+
+    def step(ev):
+        k, v = caches[it[0] % sets]
+        it[0] += 1
+        if ev:
+            ev[0].record(stream)
+        decode_token_major(q, k, v, t, workspace=ws)
+        if ev:
+            ev[1].record(stream)
+
+    wall, segs = timed(step, steps, warmup)
+    durs = [s[0] for s in segs]
+    return {"kernel_ms": dist(durs), "bytes_per_step": nbytes,
+            "roofline": roofline("hbm", nbytes, statistics.fmean(durs)),
+            "workload": {"heads": H, "kv_heads": KVH, "head_dim": Dh, "t": t,
+                         "layout": "token-major [T, KVH, Dh] fp16, fp32 q/out"}}
+
+
 # ------------------------------------------------------------ CPU baseline ---
 
 def cpu_baseline_paged(w, kind, budget_s=10.0):
@@ -293,7 +328,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="2,4,3,5,1")
+    ap.add_argument("--configs", default="2,4,3,5,1,tm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-mebibyte device buffer --steps times (the reference "
@@ -367,11 +402,22 @@ def main():
         del w5
     if "1" in cfgs:
         extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
+    if "tm" in cfgs:
+        extra["int8_engine_decode_token_major"] = bench_token_major(K, W, dev)
+        log(f"token-major decode: "
+            f"{extra['int8_engine_decode_token_major']['roofline']['achieved']} GB/s")
     torch.cuda.synchronize()
 
     if not result:  # prefill not requested: report the first measured config as headline
-        key = next(iter(extra))
-        result = extra.pop(key)
+        key = next((k for k, v in extra.items() if "value" in v), None)
+        if key is not None:
+            result = extra.pop(key)
+        else:
+            key = next(k for k, v in extra.items() if "roofline" in v)
+            result = dict(extra.pop(key))
+            result["value"] = result["roofline"]["achieved"]
+            result["unit"] = result["roofline"]["unit"]
+            result["ms_per_step"] = result["kernel_ms"]["mean"]
     decode = extra.pop("decode_cfg4", None)
     line = {
         "metric": METRIC,
