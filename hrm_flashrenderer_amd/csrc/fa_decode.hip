@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 namespace fa {
 
@@ -486,17 +487,21 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 // Merges the partials of one query row (one wave per row (b, hq, i)): the
 // workgroups whose unit range meets the row's segment are recomputed from the
 // unit prefix the decode kernel stored.
-template <int D>
+// WIDE = false: one wave per row, four rows per workgroup. WIDE = true (few
+// rows, each with many slots, as with one long sequence): one workgroup per
+// row, wave w merges slots wa + w, wa + w + 4, ..., and wave 0 merges the four
+// states.
+template <int D, bool WIDE>
 __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   constexpr int DPW = D / 64;  // d values per lane
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wave = threadIdx.x >> 6;
+  const int row = WIDE ? (int)blockIdx.x : (int)blockIdx.x * 4 + wave;
   const int lane = threadIdx.x & 63;
   const int total = p.B * p.Hq * p.M;
   if (row >= total) return;
   const int qi = row % p.M;
   const int hq = (row / p.M) % p.Hq;
   const int b = row / (p.M * p.Hq);
-  f16* op = reinterpret_cast<f16*>(p.o) + (int64_t)row * D;
 
   const int hk = p.kv_head(hq);
   float result[DPW];
@@ -523,14 +528,16 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     if (G > 0) {
       const int wa = (int)min((int64_t)W - 1, ((int64_t)(US + 1) * W - 1) / U);
       const int wb = (int)min((int64_t)W - 1, ((int64_t)UE * W - 1) / U);
+      const int first = WIDE ? wa + wave : wa;
+      constexpr int STEP = WIDE ? 4 : 1;
       // Slots in batches of 4 with every load issued before the merge; slots
       // of workgroups with an empty unit range were never written.
       constexpr int kBatch = 4;
-      for (int w0 = wa; w0 <= wb; w0 += kBatch) {
+      for (int w0 = first; w0 <= wb; w0 += kBatch * STEP) {
         float pm[kBatch], pl[kBatch], po[kBatch][DPW];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
-          const int w = w0 + i;
+          const int w = w0 + i * STEP;
           const bool live = w <= wb && (int64_t)w * U / W != (int64_t)(w + 1) * U / W;
           const int64_t srow = rbase + (int64_t)w * p.dec_rows;
           pm[i] = live ? p.ws_ml[srow * 2] : -INFINITY;
@@ -556,17 +563,44 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
         mx = bm;
       }
     }
+    if constexpr (WIDE) {
+      __shared__ float s_mx[4], s_l[4];
+      __shared__ float s_acc[4][D];
+      if (lane == 0) {
+        s_mx[wave] = mx;
+        s_l[wave] = lsum;
+      }
+#pragma unroll
+      for (int k = 0; k < DPW; ++k) s_acc[wave][lane + 64 * k] = acc[k];
+      __syncthreads();
+      if (wave != 0) return;
+      const float m_all = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+      lsum = 0.f;
+#pragma unroll
+      for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
+      if (m_all != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float sc = __builtin_amdgcn_exp2f(s_mx[w] - m_all);  // -inf slot: 0
+          lsum += sc * s_l[w];
+#pragma unroll
+          for (int k = 0; k < DPW; ++k) acc[k] += sc * s_acc[w][lane + 64 * k];
+        }
+      }
+    }
     // No visible key (lsum == 0): 0 * inf = NaN, the reference's result for a
     // fully masked row.
     const float inv = 1.f / lsum;
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = acc[k] * inv;
   }
+  if (WIDE && wave != 0) return;
   if (p.o_f32) {
     float* of = reinterpret_cast<float*>(p.o) + (int64_t)row * D;
 #pragma unroll
     for (int k = 0; k < DPW; ++k) of[lane + 64 * k] = result[k];
   } else {
+    f16* op = reinterpret_cast<f16*>(p.o) + (int64_t)row * D;
 #pragma unroll
     for (int k = 0; k < DPW; ++k) op[lane + 64 * k] = (f16)result[k];
   }
@@ -638,10 +672,21 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens)
   return plan;
 }
 
+// Rows with many partial slots (few rows: one long sequence, or a few) merge
+// with a workgroup per row; otherwise a wave per row.
+template <int D>
+void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
+  if (rows <= 512)
+    hipLaunchKernelGGL((decode_combine_kernel<D, true>), dim3((unsigned)rows), dim3(256), 0, stream,
+                       p);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<D, false>), dim3((unsigned)((rows + 3) / 4)),
+                       dim3(256), 0, stream, p);
+}
+
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
   const dim3 grid((unsigned)p.dec_wgs);
   const int rows = p.B * p.Hq * p.M;
-  const dim3 cgrid((unsigned)((rows + 3) / 4));
   const bool aligned = p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D;
   const dim3 block(kDecodeThreads);
   if (D == 128) {
@@ -651,7 +696,7 @@ hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
       hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(256), 0, stream, p);
+    launch_combine<128>(p, rows, stream);
   } else {
     if (aligned)
       hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, stream, p);
@@ -659,7 +704,7 @@ hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
       hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(256), 0, stream, p);
+    launch_combine<64>(p, rows, stream);
   }
   return hipGetLastError();
 }
