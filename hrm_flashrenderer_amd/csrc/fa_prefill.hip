@@ -428,16 +428,15 @@ __device__ __forceinline__ QuarterSrc slab_src(const AttnParams& p, int b, int h
 }
 
 // Per-wave page table in VGPR lanes: lane i holds the key-row index (element
-// offset / D) of this wave's slab of tiles base + i and base + 64 + i, or ~0u
-// when the slab has no addressable row. One vector pass (block-table loads
-// included) covers 128 tiles; a tile's lookup is then one v_readlane, so the
-// tile loop issues no scalar loads (whose lgkmcnt wait would also drain the
-// LDS reads in flight). Row indices fit 32 bits: 2^32 rows of >= 128 bytes
-// exceed the device memory.
+// offset / D) of this wave's slab of tile base + i, or ~0u when the slab has
+// no addressable row. One vector pass (block-table loads included) covers 64
+// tiles; a tile's lookup is then one v_readlane, so the tile loop issues no
+// scalar loads (whose lgkmcnt wait would also drain the LDS reads in flight).
+// Row indices fit 32 bits: 2^32 rows of >= 128 bytes exceed the device memory.
 template <int D, int NW, int BN = kBN>
 struct SlabTable {
-  static constexpr int SPAN = 128;
-  uint32_t lo, hi;
+  static constexpr int SPAN = 64;
+  uint32_t rows;
   int base;
 
   __device__ static uint32_t row(const AttnParams& p, int b, int hk, int T, int kv_len, int wave) {
@@ -447,22 +446,20 @@ struct SlabTable {
     return off < 0 ? ~0u : (uint32_t)(off / D);
   }
   __device__ void fill(const AttnParams& p, int b, int hk, int kv_len, int wave, int lane, int first) {
+    // opaque to the compiler, so it keeps no per-tile induction variables for
+    // the (rare) refill
+    asm volatile("" : "+s"(first));
     base = first;
-    lo = row(p, b, hk, first + lane, kv_len, wave);
-    hi = row(p, b, hk, first + 64 + lane, kv_len, wave);
+    rows = row(p, b, hk, first + lane, kv_len, wave);
   }
-  // Source of tile T (uniform) for this wave.
+  // Source of tile T (uniform, non-decreasing over the calls) for this wave.
   __device__ QuarterSrc get(const AttnParams& p, int b, int hk, int T, int kv_len, int wave,
                             int lane) {
-    if (T >= base + SPAN) fill(p, b, hk, kv_len, wave, lane, T);
-    const int i = T - base;
-    const uint32_t r = i < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)lo, i)
-                              : (uint32_t)__builtin_amdgcn_readlane((int)hi, i - 64);
-    const int g0 = T * BN + (BN / NW) * wave;
-    const int valid = min(BN / NW, kv_len - g0);
-    QuarterSrc q{0, 0u};
-    if (r != ~0u && valid > 0) q = QuarterSrc{(int64_t)r * D, (uint32_t)(valid * DmaCfg<D>::ROWB)};
-    return q;
+    if (T - base >= SPAN) fill(p, b, hk, kv_len, wave, lane, T);
+    const uint32_t r = (uint32_t)__builtin_amdgcn_readlane((int)rows, T - base);
+    const int valid = min(BN / NW, kv_len - (T * BN + (BN / NW) * wave));
+    const bool ok = r != ~0u && valid > 0;
+    return QuarterSrc{ok ? (int64_t)r * D : 0, ok ? (uint32_t)(valid * DmaCfg<D>::ROWB) : 0u};
   }
 };
 

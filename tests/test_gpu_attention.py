@@ -168,6 +168,20 @@ def test_prefill_tile_kernels_short_and_long_capacity(gpu, D, capacity_blocks):
     _run_and_check(c, f"non-causal cap={capacity_blocks}")
 
 
+def test_short_kernel_rows_past_one_page_table_fill(gpu):
+    """Rows of 2048 < keys <= 4096 (the 32-key-tile kernel, whose per-wave page
+    table covers 64 tiles per fill): the tiles past key 2048 come from a second
+    fill of the table, with a permuted block table, causal with offsets and
+    non-causal."""
+    prior = [2900, 1990, 3500]
+    M = 140
+    lengths = [p + M for p in prior]
+    c = _small_paged(3, 4, 1, M, lengths, seed=70, q_offsets=prior, max_blocks=256)
+    _run_and_check(c, "causal rows past 2048 keys")
+    c = _small_paged(2, 4, 2, 40, [4000, 2113], seed=71, causal=False, max_blocks=256)
+    _run_and_check(c, "non-causal rows past 2048 keys")
+
+
 def test_contiguous_long_rows(gpu):
     """Contiguous K/V longer than 4096 keys (the pipelined kernel), causal with an
     offset and non-causal, N not a multiple of the tile."""
