@@ -340,8 +340,8 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 //    ordered by (sequence, KV-head group, q tile descending, head in group):
 //    all q tiles and heads that share one KV head run on one XCD's L2, longest
 //    rows first. When every XCD owns whole (sequence, KV group) pairs, the
-//    32-key kernel orders each XCD's items by q tile descending across its
-//    pairs (longest first over the whole XCD, which shortens the tail).
+//    32-key kernel runs them two at a time with their items interleaved,
+//    longest q tile first across both, which shortens the tail.
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
@@ -796,14 +796,17 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   int qt = ntq - 1 - rem / group;
   int head = rem % group;
   if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
-    // Each XCD owns whole (sequence, KV group) pairs: run its items longest
-    // q tile first across all of them (the greedy longest-first order evens
-    // out the finishing times of the XCD's workgroup slots).
+    // Each XCD owns whole (sequence, KV group) pairs. Two pairs at a time run
+    // longest q tile first across both: the XCD's workgroup slots then finish
+    // together (a short tail), and the K/V of two pairs share the XCD's L2.
     const int kp = per_xcd / per_pair;
+    const int gp = (kp % 2 == 0) ? 2 : 1;
     const int l = slot >> 3;
-    const int band = kp * group;
-    const int r = l / band, w = l - r * band;
-    pair = (slot & 7) * kp + w / group;
+    const int gsz = gp * per_pair;
+    const int gi = l / gsz, lg = l - gi * gsz;
+    const int band = gp * group;
+    const int r = lg / band, w = lg - r * band;
+    pair = (slot & 7) * kp + gi * gp + w / group;
     qt = ntq - 1 - r;
     head = w % group;
   }
