@@ -209,6 +209,17 @@ def test_decode_m1(gpu, Hq, Hk, lengths):
     _run_and_check(c, f"decode {Hq}/{Hk}")
 
 
+@pytest.mark.parametrize("B,Hq,Hk,seed", [(8, 64, 8, 31), (13, 40, 8, 32), (1, 64, 8, 33)])
+def test_decode_combine_modes(gpu, B, Hq, Hk, seed):
+    """Both combine layouts: up to 512 query rows merge with a workgroup per
+    row (512 rows here; one 20000-key sequence, whose rows each gather many
+    partial slots), more rows with a wave per row (520 rows)."""
+    g = torch.Generator().manual_seed(seed)
+    lengths = [20000] if B == 1 else torch.randint(1, 3000, (B,), generator=g).tolist()
+    c = _small_paged(B, Hq, Hk, 1, lengths, seed=seed, causal=False)
+    _run_and_check(c, f"decode rows={B * Hq}")
+
+
 @pytest.mark.parametrize("M,causal", [(2, True), (3, False), (4, True), (16, True)])
 def test_decode_few_rows(gpu, M, causal):
     lengths = [400, 1500, 33]
