@@ -6,7 +6,7 @@
 //   O[b,h,i] = sum_j softmax_j(Q[b,h,i] . K[b,hk,j] / sqrt(D)) V[b,hk,j]
 // over keys j < N_b with k_off + j <= q_off + i when causal.
 //
-// fp16 kernels (MFMA-bound), common to all three:
+// fp16 kernels (MFMA-bound), common to both:
 //  * A workgroup owns 128 query rows of one (b, hq): 4 waves x 32 rows. Q stays
 //    in registers as the B operand of S^T = K Q^T (v_mfma_f32_32x32x16_f16).
 //  * Both products keep the query row as the MFMA column: every lane owns one
@@ -18,11 +18,11 @@
 //  * Causal tiles beyond the diagonal are never loaded; waves whose rows see
 //    none of a tile skip its math; the q-tile order is reversed so the longest
 //    rows start first.
-// Kernels: prefill_pipe_kernel and prefill_b32_kernel stream K/V tiles into
-// LDS by DMA (pages of a multiple of 16 tokens, or contiguous K/V; see the
-// section below); prefill_f16_kernel stages tiles through registers and looks
-// up every key row on its own (any page size); prefill_f32_kernel is the
-// exact-fp32 contiguous op.
+// Kernels: prefill_b32_kernel streams K/V tiles into LDS by DMA (pages of a
+// multiple of 16 tokens, or contiguous K/V; see the section below);
+// prefill_f16_kernel stages tiles through registers and looks up every key
+// row on its own (any page size); prefill_f32_kernel is the exact-fp32
+// contiguous op.
 //
 // prefill_f16_kernel: the next 64-key tile's rows are fetched from HBM into
 // registers while the current tile is computed. K is stored row-major
@@ -31,8 +31,6 @@
 // LDS reads per MFMA.
 #include "fa_common.h"
 
-#include <stdlib.h>
-#include <string.h>
 
 #include <type_traits>
 
@@ -314,9 +312,8 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile-DMA prefill kernels (pages of a multiple of 16 tokens, or contiguous
-// K/V): prefill_pipe_kernel (64-key tiles) and prefill_b32_kernel (32-key
-// tiles). Common design:
+// Tile-DMA prefill kernel (pages of a multiple of 16 tokens, or contiguous
+// K/V): prefill_b32_kernel (32-key tiles). Design:
 //
 //  * K and V tiles go from HBM straight into LDS with buffer_load ... lds
 //    (16 bytes per lane), no staging registers. Each wave moves one slab of
@@ -373,9 +370,7 @@ template <int D>
 struct DmaCfg {
   static constexpr int ROWB = 2 * D;             // bytes per key row
   static constexpr int CH = D / 8;               // 16-byte chunks per row
-  static constexpr int TILE = kBN * ROWB;        // bytes per K (or V) tile
   static constexpr int RPI = 1024 / ROWB;        // rows per wave-wide 16-byte load
-  static constexpr int IPQ = 16 / RPI;           // loads per 16-key quarter
   __device__ static int swz_k(int row) { return row % CH; }
   __device__ static int swz_v(int row) { return (4 * row) % CH; }
 };
@@ -405,27 +400,12 @@ __device__ __forceinline__ half8 ld_vt(const char* buf, const int* voff, int s, 
 // With NW waves per workgroup and BN-key tiles, wave w moves the slab of
 // SLAB = BN / NW keys starting at k0 + SLAB * w (one page: pages hold a
 // multiple of 16 tokens).
-template <int D, int NW, int BN = kBN>
+template <int D, int NW, int BN>
 struct Slab {
   static constexpr int SLAB = BN / NW;                  // keys per wave and tile
   static constexpr int IPW = SLAB / DmaCfg<D>::RPI;     // 16-byte DMA loads per wave
   static_assert(IPW >= 1, "slab smaller than one wave-wide load");
 };
-
-template <int D, int NW, int BN = kBN>
-__device__ __forceinline__ QuarterSrc slab_src(const AttnParams& p, int b, int hk, int k0,
-                                               int kv_len, int wave) {
-  using C = DmaCfg<D>;
-  constexpr int SLAB = BN / NW;
-  const int g0 = k0 + SLAB * wave;
-  const int valid = min(SLAB, kv_len - g0);
-  QuarterSrc q{0, 0u};
-  if (valid > 0) {
-    const int64_t off = p.kv.row_offset(b, hk, g0);
-    if (off >= 0) q = QuarterSrc{off, (uint32_t)(valid * C::ROWB)};
-  }
-  return q;
-}
 
 // Per-wave page table in VGPR lanes: lane i holds the key-row index (element
 // offset / D) of this wave's slab of tile base + i, or ~0u when the slab has
@@ -433,7 +413,7 @@ __device__ __forceinline__ QuarterSrc slab_src(const AttnParams& p, int b, int h
 // tiles; a tile's lookup is then one v_readlane, so the tile loop issues no
 // scalar loads (whose lgkmcnt wait would also drain the LDS reads in flight).
 // Row indices fit 32 bits: 2^32 rows of >= 128 bytes exceed the device memory.
-template <int D, int NW, int BN = kBN>
+template <int D, int NW, int BN>
 struct SlabTable {
   static constexpr int SPAN = 64;
   uint32_t rows;
@@ -463,13 +443,13 @@ struct SlabTable {
   }
 };
 
-template <int D, int NW, int BN = kBN>
+template <int D, int NW, int BN>
 struct SlabLane {
   uint32_t vk[Slab<D, NW, BN>::IPW];
   uint32_t vv[Slab<D, NW, BN>::IPW];
 };
 
-template <int D, int NW, int BN = kBN>
+template <int D, int NW, int BN>
 __device__ __forceinline__ SlabLane<D, NW, BN> slab_lane(int wave, int lane) {
   using C = DmaCfg<D>;
   SlabLane<D, NW, BN> d;
@@ -484,7 +464,7 @@ __device__ __forceinline__ SlabLane<D, NW, BN> slab_lane(int wave, int lane) {
   return d;
 }
 
-template <int D, int NW, int BN = kBN>
+template <int D, int NW, int BN>
 __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* voffs,
                                          const char* base, int wave, char* dst_tile) {
   using C = DmaCfg<D>;
@@ -495,285 +475,9 @@ __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* vo
 }
 
 // ---------------------------------------------------------------------------
-// Software-pipelined prefill on 64-key tiles, two workgroups of four waves
-// (128 query rows) per CU. K runs one tile ahead of V so that each wave
-// overlaps its vector and matrix work:
-//   iteration t:  exp2 of S_t (VALU)  with  S_{t+1} = K_{t+1} Q^T (MFMA)
-//                 then O^T += V_t^T P_t^T (MFMA)
-// LDS: K buffers at 0 and TILE, V buffers at 2*TILE and 3*TILE. At iteration t
-// (parity PB = t & 1) the wave reads K_{t+1} from K[PB^1] and V_t from V[PB],
-// while the DMA fills K[PB] with K_{t+2} and V[PB^1] with V_{t+1}.
-// ---------------------------------------------------------------------------
-
-// Row-limit mask of one 64-key tile of S^T (keys k0 + 8(r/4) + 4*half + r%4,
-// +32 for the second block).
-__device__ __forceinline__ void mask_tile(floatx16& s0, floatx16& s1, int k0, int half_id, int lim) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int key = k0 + 8 * (r >> 2) + 4 * half_id + (r & 3);
-    if (key >= lim) s0[r] = -INFINITY;
-    if (key + 32 >= lim) s1[r] = -INFINITY;
-  }
-}
-
-__device__ __forceinline__ float tile_max(const floatx16& s0, const floatx16& s1) {
-  return fmaxf(max16(s0), max16(s1));
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void prefill_pipe_kernel(AttnParams p, int ntq,
-                                                                   int group, int per_xcd,
-                                                                   int total) {
-  using C = DmaCfg<D>;
-  constexpr int NW = kThreads / 64;
-  constexpr int BM = kBM;
-  constexpr int KSTEPS = D / 16;
-  constexpr int DBLK = D / 32;
-  constexpr int EPK = 32 / KSTEPS;  // exp2 elements per k-step (over both halves)
-  __shared__ __attribute__((aligned(1024))) char smem[4 * C::TILE];  // K0 K1 V0 V1
-
-  // ---- work item (XCD-aware order) ----
-  const int slot = blockIdx.x;
-  const int item = (slot & 7) * per_xcd + (slot >> 3);
-  if (item >= total) return;
-  const int per_pair = ntq * group;
-  const int pair = item / per_pair;
-  const int rem = item - pair * per_pair;
-  const int qt = ntq - 1 - rem / group;
-  const int ngroups = p.Hq / group;
-  const int hq = (pair % ngroups) * group + rem % group;
-  const int b = pair / ngroups;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31;
-  const int half_id = lane >> 5;
-  const int q0 = qt * BM;
-  const int qrow = q0 + wave * 32 + col;
-  f16* op = reinterpret_cast<f16*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
-
-  const int hk = p.kv_head(hq);
-  if (hk < 0) {
-    if (qrow < p.M) {
-      for (int d = half_id * (D / 2); d < (half_id + 1) * (D / 2); ++d)
-        op[(int64_t)qrow * D + d] = (f16)__builtin_nanf("");
-    }
-    return;
-  }
-
-  const int kv_len = p.kv_len(b);
-  const int qo = p.q_off(b);
-  const int ko = p.k_off(b);
-  const int last_row = min(q0 + BM, p.M) - 1;
-  const int wg_lim = row_key_limit(kv_len, p.causal, qo, ko, last_row);
-  const int ntiles = (wg_lim + kBN - 1) / kBN;
-  const int wrow0 = q0 + wave * 32;
-  const int wrow1 = min(wrow0 + 31, p.M - 1);
-  const bool wave_rows = wrow0 < p.M;
-  const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
-  const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
-  const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
-
-  const char* kp = reinterpret_cast<const char*>(p.k);
-  const char* vp = reinterpret_cast<const char*>(p.v);
-  const SlabLane<D, NW> dl = slab_lane<D, NW>(wave, lane);
-  char* const kbuf0 = smem;
-  char* const vbuf0 = smem + 2 * C::TILE;
-
-  // Prologue DMA: K_0, V_0, K_1. src_a / src_b: pages of tiles t+1 / t+2.
-  QuarterSrc src_a = slab_src<D, NW>(p, b, hk, kBN, kv_len, wave);
-  QuarterSrc src_b = slab_src<D, NW>(p, b, hk, 2 * kBN, kv_len, wave);
-  if (ntiles > 0) {
-    const QuarterSrc s0 = slab_src<D, NW>(p, b, hk, 0, kv_len, wave);
-    dma_slab<D, NW>(s0, dl.vk, kp, wave, kbuf0);
-    dma_slab<D, NW>(s0, dl.vv, vp, wave, vbuf0);
-    if (ntiles > 1) dma_slab<D, NW>(src_a, dl.vk, kp, wave, kbuf0 + C::TILE);
-  }
-
-  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
-  half8 qreg[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    qreg[ks] = qrow < p.M
-                   ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
-                   : half8{0, 0, 0, 0, 0, 0, 0, 0};
-  }
-  if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
-
-  int koff[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks)
-    koff[ks] = col * C::ROWB + 16 * ((2 * ks + half_id) ^ C::swz_k(col));
-  const int gq = lane >> 4, sl = lane & 15;
-  const int vrow = 4 * (gq >> 1) + (sl >> 2);
-  int voff[DBLK];  // relative to the V tile
-#pragma unroll
-  for (int i = 0; i < DBLK; ++i) {
-    const int d = 32 * i + 16 * (gq & 1) + 4 * (sl & 3);
-    voff[i] = vrow * C::ROWB + 16 * ((d >> 3) ^ C::swz_v(vrow)) + 2 * (d & 7);
-  }
-
-  floatx16 acc_o[DBLK];
-#pragma unroll
-  for (int i = 0; i < DBLK; ++i) acc_o[i] = floatx16{};
-  float m_ref = -INFINITY;  // scaled (log2) reference max
-  float l_run = 0.f;
-  const float c = p.scale_log2;
-  const half2v ones = half2v{(f16)1.f, (f16)1.f};
-  constexpr int KA = 2;
-
-  // S^T of one tile from LDS (plain, used for tile 0).
-  auto qk_plain = [&](const char* kb, floatx16& s0, floatx16& s1) {
-    s0 = floatx16{};
-    s1 = floatx16{};
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      const half8 a0 = *reinterpret_cast<const half8*>(kb + koff[ks]);
-      const half8 a1 = *reinterpret_cast<const half8*>(kb + koff[ks] + 32 * C::ROWB);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qreg[ks], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qreg[ks], s1, 0, 0, 0);
-    }
-  };
-
-  // Two S^T register sets, used alternately by even and odd tiles.
-  floatx16 sa0, sa1, sb0, sb1;
-  if (ntiles > 0) {
-    // K_0 has landed when at most the loads issued after it are in flight.
-    if (ntiles > 1)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Slab<D, NW>::IPW) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Slab<D, NW>::IPW) : "memory");
-    __syncthreads();
-    if (0 < wave_lim_max) qk_plain(kbuf0, sa0, sa1);
-  }
-
-  // Iteration t: softmax of tile t, S^T of tile t+1 (if NEXT), PV of tile t.
-  // The exp2 block and the PV product share one basic block (the mask and the
-  // rescale, which branch, come first), so the exp2 values are not sunk into
-  // the PV block and the per-k-step groups below keep VALU and MFMA work
-  // interleaved.
-  auto step = [&](auto par, auto has_next, int t) {
-    constexpr int PB = decltype(par)::value;
-    constexpr bool NEXT = decltype(has_next)::value;
-    floatx16& c0 = PB ? sb0 : sa0;  // S^T of tile t
-    floatx16& c1 = PB ? sb1 : sa1;
-    floatx16& n0 = PB ? sa0 : sb0;  // S^T of tile t+1
-    floatx16& n1 = PB ? sa1 : sb1;
-    const int k0 = t * kBN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 2 < ntiles) dma_slab<D, NW>(src_b, dl.vk, kp, wave, kbuf0 + PB * C::TILE);
-    if (t + 1 < ntiles) dma_slab<D, NW>(src_a, dl.vv, vp, wave, vbuf0 + (PB ^ 1) * C::TILE);
-    src_a = src_b;
-    src_b = slab_src<D, NW>(p, b, hk, k0 + 3 * kBN, kv_len, wave);
-    if (k0 >= wave_lim_max) return;
-
-    // Mask (diagonal or last tile), row max over both lane halves, lazy rescale.
-    if (k0 + kBN > wave_lim_min) mask_tile(c0, c1, k0, half_id, lim);
-    float mx_cur;
-    {
-      const float m = tile_max(c0, c1);
-      const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m),
-                                                       __builtin_bit_cast(uint32_t, m), false, false);
-      mx_cur = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]),
-                     __builtin_bit_cast(float, (uint32_t)sw[1])) * c;
-    }
-    if (__builtin_amdgcn_ballot_w64(mx_cur > m_ref + kRescaleLog2) != 0) {
-      const float m_new = fmaxf(m_ref, mx_cur);
-      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DBLK; ++i) acc_o[i] = acc_o[i] * alpha;
-      m_ref = m_new;
-    }
-    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-
-    // exp2 of S_t (32 values per lane) with the MFMAs of S_{t+1}: keys 0..31
-    // of tile t+1 (n0) while the first half of S_t is exponentiated, keys
-    // 32..63 (n1) during the second half, so at most three 16-register S
-    // blocks are live at a time.
-    half8 pb[4];
-    float ps[2] = {0.f, 0.f};  // two independent row-sum chains
-    const char* kb = kbuf0 + (PB ^ 1) * C::TILE;
-    auto half_block = [&](floatx16& nacc, const floatx16& cur, int kbase, int pbase) {
-      half8 ka[KA];
-      if constexpr (NEXT) {
-        nacc = floatx16{};
-#pragma unroll
-        for (int i = 0; i < KA; ++i) ka[i] = *reinterpret_cast<const half8*>(kb + koff[i] + kbase);
-      }
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        if constexpr (NEXT) {
-          nacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % KA], qreg[ks], nacc, 0, 0, 0);
-          if (ks + KA < KSTEPS) ka[ks % KA] = *reinterpret_cast<const half8*>(kb + koff[ks + KA] + kbase);
-        }
-#pragma unroll
-        for (int e = 0; e < EPK / 2; e += 2) {
-          const int idx = ks * (EPK / 2) + e;  // 0..15 within cur
-          const f16 e0 = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(cur[idx], c, -m_use));
-          const f16 e1 = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(cur[idx + 1], c, -m_use));
-          pb[pbase + (idx >> 3)][idx & 7] = e0;
-          pb[pbase + (idx >> 3)][(idx & 7) + 1] = e1;
-          ps[ks & 1] = __builtin_amdgcn_fdot2(half2v{e0, e1}, ones, ps[ks & 1], false);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    half_block(n0, c0, 0, 0);
-    half_block(n1, c1, 32 * C::ROWB, 2);
-    l_run += ps[0] + ps[1];
-
-    // O^T += V_t^T P_t^T: operands read VA MFMAs ahead.
-    const char* vb = vbuf0 + PB * C::TILE;
-    constexpr int NMF = 4 * DBLK;
-    constexpr int VA = 3;
-    half8 va[VA];
-#pragma unroll
-    for (int m = 0; m < VA; ++m) va[m] = ld_vt<D>(vb, voff, m / DBLK, m % DBLK);
-#pragma unroll
-    for (int m = 0; m < NMF; ++m) {
-      const int st = m / DBLK, i = m % DBLK;
-      acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[m % VA], pb[st], acc_o[i], 0, 0, 0);
-      if (m + VA < NMF) va[m % VA] = ld_vt<D>(vb, voff, (m + VA) / DBLK, (m + VA) % DBLK);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  int t = 0;
-  for (; t + 2 < ntiles; t += 2) {
-    step(std::integral_constant<int, 0>{}, std::true_type{}, t);
-    step(std::integral_constant<int, 1>{}, std::true_type{}, t + 1);
-  }
-  if (t + 1 < ntiles) {
-    step(std::integral_constant<int, 0>{}, std::true_type{}, t);
-    step(std::integral_constant<int, 1>{}, std::false_type{}, t + 1);
-  } else if (t < ntiles) {
-    step(std::integral_constant<int, 0>{}, std::false_type{}, t);
-  }
-
-  if (qrow >= p.M) return;
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
-  f16* orow = op + (int64_t)qrow * D;
-#pragma unroll
-  for (int i = 0; i < DBLK; ++i) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
-                            (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
-      *reinterpret_cast<half4*>(orow + 32 * i + 8 * g + 4 * half_id) = h;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Prefill on 32-key tiles: 16 KB of K and V per stage, two stages per
 // workgroup (32 KB), at most 168 VGPRs, so three workgroups (three waves per
-// SIMD) share a CU. Without the K-ahead pipeline (which needs more registers
-// than three waves per SIMD leave), but with more waves to hide latency; it
-// wins on short rows, where per-workgroup start-up weighs more.
+// SIMD) share a CU, whose waves hide each other's latency.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, int ntq,
@@ -1080,22 +784,6 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(AttnParams p) {
 
 }  // namespace
 
-// Kernel choice for page sizes that are a multiple of 16 (and contiguous K/V):
-// short rows (capacity <= 4096 keys) run the 32-key-tile kernel, whose three
-// workgroups per CU hide more latency; long rows run the pipelined 64-key
-// kernel, which overlaps softmax and matrix work within a wave.
-// FA_PREFILL_KERNEL=pipe|b32 forces one of them.
-enum class PrefillKernel { kPipe, kB32 };
-
-PrefillKernel choose_prefill(const AttnParams& p) {
-  static const char* force = getenv("FA_PREFILL_KERNEL");
-  if (force != nullptr) {
-    if (strcmp(force, "pipe") == 0) return PrefillKernel::kPipe;
-    if (strcmp(force, "b32") == 0) return PrefillKernel::kB32;
-  }
-  return p.N <= 4096 ? PrefillKernel::kB32 : PrefillKernel::kPipe;
-}
-
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream) {
   if (dtype == 1) {
     const dim3 grid((unsigned)((p.M + 63) / 64), (unsigned)p.Hq, (unsigned)p.B);
@@ -1119,21 +807,12 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
   const int total = ntq * p.Hq * p.B;
   const int per_xcd = (total + 7) / 8;
   const dim3 grid((unsigned)(8 * per_xcd));
-  if (choose_prefill(p) == PrefillKernel::kB32) {
-    if (D == 128)
-      hipLaunchKernelGGL(prefill_b32_kernel<128>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                         per_xcd, total);
-    else
-      hipLaunchKernelGGL(prefill_b32_kernel<64>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                         per_xcd, total);
-  } else {
-    if (D == 128)
-      hipLaunchKernelGGL(prefill_pipe_kernel<128>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                         per_xcd, total);
-    else
-      hipLaunchKernelGGL(prefill_pipe_kernel<64>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                         per_xcd, total);
-  }
+  if (D == 128)
+    hipLaunchKernelGGL(prefill_b32_kernel<128>, grid, dim3(kThreads), 0, stream, p, ntq, group,
+                       per_xcd, total);
+  else
+    hipLaunchKernelGGL(prefill_b32_kernel<64>, grid, dim3(kThreads), 0, stream, p, ntq, group,
+                       per_xcd, total);
   return hipGetLastError();
 }
 

@@ -154,9 +154,8 @@ def test_paged_prefill_gqa_block_table(gpu, D):
 @pytest.mark.parametrize("capacity_blocks", [None, 300])
 @pytest.mark.parametrize("D", [64, 128])
 def test_prefill_tile_kernels_short_and_long_capacity(gpu, D, capacity_blocks):
-    """The same inputs through both DMA prefill kernels: a block table of at most
-    4096 keys of capacity selects the 32-key-tile kernel, a wider one (300 pages
-    of 16 = 4800 keys) the pipelined 64-key-tile kernel."""
+    """The DMA prefill kernel with a block table of at most 4096 keys of
+    capacity and with a wider one (300 pages of 16 = 4800 keys)."""
     prior = [0, 133, 0, 61]
     M = 200
     lengths = [p + M for p in prior]
@@ -183,7 +182,7 @@ def test_short_kernel_rows_past_one_page_table_fill(gpu):
 
 
 def test_contiguous_long_rows(gpu):
-    """Contiguous K/V longer than 4096 keys (the pipelined kernel), causal with an
+    """Contiguous K/V longer than 4096 keys, causal with an
     offset and non-causal, N not a multiple of the tile."""
     B, Hq, Hk, M, N, D = 1, 4, 2, 96, 4203, 128
     q, k, v = seeded((B, Hq, M, D), 60), seeded((B, Hk, N, D), 61), seeded((B, Hk, N, D), 62)
