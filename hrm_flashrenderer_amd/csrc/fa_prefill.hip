@@ -336,9 +336,11 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 //    the 8 XCDs, so slot L runs item (L % 8) * per_xcd + L / 8 of a list
 //    ordered by (sequence, KV-head group, q tile descending, head in group):
 //    all q tiles and heads that share one KV head run on one XCD's L2, longest
-//    rows first. When every XCD owns whole (sequence, KV group) pairs, the
-//    32-key kernel runs them two at a time with their items interleaved,
-//    longest q tile first across both, which shortens the tail.
+//    rows first. When the (sequence, KV group) pairs divide evenly over the
+//    XCDs, XCD x owns pairs x, x + 8, ... (each XCD gets a share of every
+//    sequence length), runs them longest sequence first, two at a time with
+//    their items interleaved, longest q tile first across both, which
+//    shortens the tail.
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
@@ -354,6 +356,22 @@ __device__ __forceinline__ float max16(const floatx16& s) {
   const float a4 = max3f(s[12], s[13], s[14]);
   const float b0 = max3f(a0, a1, a2), b1 = max3f(a3, a4, s[15]);
   return fmaxf(b0, b1);
+}
+
+// Index i of pair x + 8i among the kp pairs of XCD x, at position j when those
+// pairs are ordered by key count, longest first, ties by index. Each lane
+// ranks one pair against all kp (kp <= 64); the result is wave-uniform.
+__device__ __forceinline__ int pair_by_length(const AttnParams& p, int x, int kp, int ngroups,
+                                              int j) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane < kp ? p.kv_len((x + 8 * lane) / ngroups) : -1;
+  int rank = 0;
+  for (int i = 0; i < kp; ++i) {
+    const int m = __builtin_amdgcn_readlane(n, i);
+    rank += (m > n || (m == n && i < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __ballot(lane < kp && rank == j);
+  return __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -499,22 +517,26 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   int rem = item - pair * per_pair;
   int qt = ntq - 1 - rem / group;
   int head = rem % group;
+  const int ngroups = p.Hq / group;
   if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
-    // Each XCD owns whole (sequence, KV group) pairs. Two pairs at a time run
+    // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
+    // x + 8, x + 16, ..., so sequences of different lengths spread over all
+    // XCDs, in order of key count, longest first. Two pairs at a time run
     // longest q tile first across both: the XCD's workgroup slots then finish
     // together (a short tail), and the K/V of two pairs share the XCD's L2.
     const int kp = per_xcd / per_pair;
     const int gp = (kp % 2 == 0) ? 2 : 1;
-    const int l = slot >> 3;
+    const int x = slot & 7, l = slot >> 3;
     const int gsz = gp * per_pair;
     const int gi = l / gsz, lg = l - gi * gsz;
     const int band = gp * group;
     const int r = lg / band, w = lg - r * band;
-    pair = (slot & 7) * kp + gi * gp + w / group;
+    int j = gi * gp + w / group;
+    if (p.seqlen != nullptr && kp > 1 && kp <= 64) j = pair_by_length(p, x, kp, ngroups, j);
+    pair = x + 8 * j;
     qt = ntq - 1 - r;
     head = w % group;
   }
-  const int ngroups = p.Hq / group;
   const int hq = (pair % ngroups) * group + head;
   const int b = pair / ngroups;
 

@@ -192,6 +192,21 @@ def test_contiguous_long_rows(gpu):
                      f"long rows causal={causal} qo={qo}")
 
 
+@pytest.mark.parametrize("B,Hq,Hk,M,seed", [(16, 8, 1, 64, 80), (6, 16, 4, 100, 81),
+                                             (8, 64, 8, 128, 82), (72, 8, 8, 16, 83)])
+def test_ragged_lengths_every_head(gpu, B, Hq, Hk, M, seed):
+    """Sequences of different lengths whose (sequence, KV group) pairs divide
+    over the 8 XCDs (2, 3 and 8 pairs per XCD, ordered by length with ties;
+    72 per XCD, kept in index order): every head of every sequence is checked,
+    so a pair run twice or never shows."""
+    g = torch.Generator().manual_seed(seed)
+    prior = torch.randint(0, 700, (B,), generator=g).tolist()
+    prior[1] = prior[0]
+    lengths = [p + M for p in prior]
+    c = _small_paged(B, Hq, Hk, M, lengths, seed=seed, q_offsets=prior)
+    _run_and_check(c, f"ragged B={B} Hq={Hq} Hk={Hk}")
+
+
 def test_chunked_prefill_per_sequence_offsets(gpu):
     prior = [0, 37, 150, 600]
     M = 130
