@@ -703,18 +703,36 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     if (t + 1 < ntiles) step(std::integral_constant<int, 1>{}, t + 1);
   }
 
-  if (qrow >= p.M) return;
+  // O leaves through LDS (128 rows x 2D bytes, the size of the two K/V
+  // stages, with K's chunk swizzle): each wave writes its 32 rows as fp16,
+  // then each thread stores whole 16-byte chunks, 16 threads per row, so one
+  // store instruction writes 4 complete rows instead of a 16-byte piece of
+  // each of 32 rows (with the non-temporal store below: +4.5 % on cfg2).
+  // Lane (col, half) holds d = 32i + 8g + 4*half + 0..3 of its row, i.e.
+  // half of 16-byte chunk 4i + g.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
-  f16* orow = op + (int64_t)qrow * D;
+  __syncthreads();  // every wave has finished reading the last K/V stage
+  const int lrow = wave * 32 + col;
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
                             (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
-      *reinterpret_cast<half4*>(orow + 32 * i + 8 * g + 4 * half_id) = h;
+      const int chunk = (4 * i + g) ^ C::swz_k(lrow);
+      *reinterpret_cast<half4*>(smem + lrow * C::ROWB + 16 * chunk + 8 * half_id) = h;
     }
+  }
+  __syncthreads();
+  const int rows = min(kBM, p.M - q0);
+  f16* ob = op + (int64_t)q0 * D;
+  for (int e = tid; e < rows * C::CH; e += kThreads) {
+    const int r = e / C::CH, ch = e % C::CH;
+    const half8 v = *reinterpret_cast<const half8*>(smem + r * C::ROWB + 16 * (ch ^ C::swz_k(r)));
+    // O is not read again by this kernel: a non-temporal store keeps the
+    // K/V lines that other workgroups still read in L2.
+    __builtin_nontemporal_store(v, reinterpret_cast<half8*>(ob + (int64_t)r * D + 8 * ch));
   }
 }
 
