@@ -358,13 +358,39 @@ __device__ __forceinline__ float max16(const floatx16& s) {
   return fmaxf(b0, b1);
 }
 
+// Per-sequence data of the prefill kernels, loaded without a branch on the
+// optional arrays (a branch would make the compiler wait for each load before
+// the next one): a missing array reads a valid stand-in address (the first
+// word of Q) and its default replaces the value. Uniform (b, hq) give scalar
+// loads; per-lane ones give vector loads that all leave before one wait.
+struct SeqData {
+  int kv_len, hk, qo, ko;
+};
+
+__device__ __forceinline__ int ld_or(const int32_t* ptr, int idx, int dflt, const void* any) {
+  typedef const __attribute__((address_space(4))) int32_t cint;
+  const int32_t* a = ptr != nullptr ? ptr + idx : reinterpret_cast<const int32_t*>(any);
+  const int v = *(cint*)a;
+  return ptr != nullptr ? v : dflt;
+}
+
+__device__ __forceinline__ SeqData seq_data(const AttnParams& p, int b, int hq) {
+  SeqData d;
+  const int n = ld_or(p.seqlen, b, p.N, p.q);
+  d.kv_len = n < 0 ? 0 : n > p.N ? p.N : n;
+  const int hk = ld_or(p.head_map, hq, p.head_mod ? hq % p.Hk : hq / p.group, p.q);
+  d.hk = (hk >= 0 && hk < p.Hk) ? hk : -1;
+  d.qo = ld_or(p.q_offsets, b, p.q_offset, p.q);
+  d.ko = ld_or(p.k_offsets, b, p.k_offset, p.q);
+  return d;
+}
+
 // Index i of pair x + 8i among the kp pairs of XCD x, at position j when those
-// pairs are ordered by key count, longest first, ties by index. Each lane
-// ranks one pair against all kp (kp <= 64); the result is wave-uniform.
-__device__ __forceinline__ int pair_by_length(const AttnParams& p, int x, int kp, int ngroups,
-                                              int j) {
+// pairs are ordered by key count, longest first, ties by index. Lane i holds
+// n = key count of pair x + 8i (-1 for lanes >= kp) and ranks it against all
+// kp (kp <= 64); the result is wave-uniform.
+__device__ __forceinline__ int pair_by_length(int n, int kp, int j) {
   const int lane = threadIdx.x & 63;
-  const int n = lane < kp ? p.kv_len((x + 8 * lane) / ngroups) : -1;
   int rank = 0;
   for (int i = 0; i < kp; ++i) {
     const int m = __builtin_amdgcn_readlane(n, i);
@@ -434,30 +460,85 @@ struct Slab {
 template <int D, int NW, int BN>
 struct SlabTable {
   static constexpr int SPAN = 64;
-  uint32_t rows;
+  uint32_t rows;     // pool row of the slab of tile base + lane, KV head 0 (~0u: none)
   int base;
+  uint32_t hk_rows;  // rows between KV heads: hk * stride_hk / D
 
-  __device__ static uint32_t row(const AttnParams& p, int b, int hk, int T, int kv_len, int wave) {
+  // Page row of the slab of tile T for KV head 0, whether or not it holds
+  // keys below kv_len (get() masks by kv_len): the table load needs only b,
+  // so it leaves with the Q loads, before kv_len and the head map are known.
+  // row_offset bounds the page by the block table width.
+  // The same map as KVMap::row_offset (KV head 0), split into the table load
+  // (row_load) and the arithmetic on its result (row_finish), with the
+  // per-lane checks as selects around an always in-bounds load: no divergent
+  // branch makes the compiler wait for the load where it is issued, and the
+  // first fill can issue it, then other loads, then finish.
+  struct RowReq {
+    unsigned raw;   // physical page id (block table), logical page, or token
+    unsigned slot;  // token within the page
+    bool ok;
+  };
+  __device__ static RowReq row_load(const AttnParams& p, int b, int T, int wave) {
+    const KVMap& kv = p.kv;
     const int g0 = T * BN + (BN / NW) * wave;
-    if (g0 < 0 || g0 >= kv_len) return ~0u;
-    const int64_t off = p.kv.row_offset(b, hk, g0);
-    return off < 0 ? ~0u : (uint32_t)(off / D);
+    RowReq r;
+    r.ok = g0 >= 0 && g0 < p.N;
+    const unsigned g = r.ok ? (unsigned)g0 : 0u;
+    if (!kv.paged) {
+      r.raw = g;
+      r.slot = 0;
+      return r;
+    }
+    unsigned page;
+    if (kv.ps_shift >= 0) {
+      page = g >> kv.ps_shift;
+      r.slot = g & (unsigned)(kv.PS - 1);
+    } else {
+      page = g / (unsigned)kv.PS;
+      r.slot = g - page * (unsigned)kv.PS;
+    }
+    r.ok = r.ok && page < (unsigned)kv.max_blocks;
+    const unsigned pg = r.ok ? page : 0u;
+    if (kv.block_table != nullptr) {
+      typedef const __attribute__((address_space(4))) int32_t ctable;
+      r.raw = (unsigned)((ctable*)kv.block_table)[(int64_t)b * kv.max_blocks + pg];
+    } else {
+      r.raw = pg;
+    }
+    return r;
   }
-  __device__ void fill(const AttnParams& p, int b, int hk, int kv_len, int wave, int lane, int first) {
+  __device__ static uint32_t row_finish(const AttnParams& p, int b, const RowReq& r) {
+    const KVMap& kv = p.kv;
+    if (!kv.paged)
+      return r.ok ? (uint32_t)(((int64_t)b * kv.stride_nb + (int64_t)r.raw * kv.stride_tok) / D) : ~0u;
+    bool ok = r.ok;
+    unsigned nb, pp;
+    if (kv.block_table != nullptr) {
+      ok = ok && r.raw < (unsigned)kv.num_phys;
+      nb = kv.num_phys <= kv.P ? 0u : r.raw / (unsigned)kv.P;
+      pp = r.raw - nb * (unsigned)kv.P;
+    } else {
+      nb = (unsigned)b;
+      pp = r.raw;
+    }
+    const int64_t off = (int64_t)nb * kv.stride_nb + (int64_t)pp * kv.stride_page + (int64_t)r.slot * D;
+    return ok ? (uint32_t)(off / D) : ~0u;
+  }
+  __device__ void fill(const AttnParams& p, int b, int wave, int lane, int first) {
     // opaque to the compiler, so it keeps no per-tile induction variables for
     // the (rare) refill
     asm volatile("" : "+s"(first));
     base = first;
-    rows = row(p, b, hk, first + lane, kv_len, wave);
+    rows = row_finish(p, b, row_load(p, b, first + lane, wave));
   }
   // Source of tile T (uniform, non-decreasing over the calls) for this wave.
-  __device__ QuarterSrc get(const AttnParams& p, int b, int hk, int T, int kv_len, int wave,
-                            int lane) {
-    if (T - base >= SPAN) fill(p, b, hk, kv_len, wave, lane, T);
+  __device__ QuarterSrc get(const AttnParams& p, int b, int T, int kv_len, int wave, int lane) {
+    if (T - base >= SPAN) fill(p, b, wave, lane, T);
     const uint32_t r = (uint32_t)__builtin_amdgcn_readlane((int)rows, T - base);
     const int valid = min(BN / NW, kv_len - (T * BN + (BN / NW) * wave));
     const bool ok = r != ~0u && valid > 0;
-    return QuarterSrc{ok ? (int64_t)r * D : 0, ok ? (uint32_t)(valid * DmaCfg<D>::ROWB) : 0u};
+    return QuarterSrc{ok ? (int64_t)(r + hk_rows) * D : 0,
+                      ok ? (uint32_t)(valid * DmaCfg<D>::ROWB) : 0u};
   }
 };
 
@@ -518,12 +599,16 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   int qt = ntq - 1 - rem / group;
   int head = rem % group;
   const int ngroups = p.Hq / group;
+  // With `pre`, the sequence data of the chosen pair come from the loads that
+  // ordered the pairs (kv_len_pre, hk_pre, qo_pre, ko_pre).
+  bool pre = false;
+  int kv_len_pre = 0, hk_pre = 0, qo_pre = 0, ko_pre = 0;
   if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
     // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
     // x + 8, x + 16, ..., so sequences of different lengths spread over all
-    // XCDs, in order of key count, longest first. Two pairs at a time run
-    // longest q tile first across both: the XCD's workgroup slots then finish
-    // together (a short tail), and the K/V of two pairs share the XCD's L2.
+    // XCDs. Two pairs at a time run longest q tile first across both: the
+    // XCD's workgroup slots then finish together (a short tail), and the K/V
+    // of two pairs share the XCD's L2.
     const int kp = per_xcd / per_pair;
     const int gp = (kp % 2 == 0) ? 2 : 1;
     const int x = slot & 7, l = slot >> 3;
@@ -532,7 +617,22 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     const int band = gp * group;
     const int r = lg / band, w = lg - r * band;
     int j = gi * gp + w / group;
-    if (p.seqlen != nullptr && kp > 1 && kp <= 64) j = pair_by_length(p, x, kp, ngroups, j);
+    if (p.seqlen != nullptr && p.q_offsets != nullptr && kp > 1 && kp <= 64) {
+      // Chunked prefill over cached context: a pair's work grows with its
+      // sequence's key count, so the XCD runs its pairs longest first. One
+      // round of per-lane loads gives every candidate's key count, head map
+      // entry and offsets; the chosen pair's are then read from its lane. (A
+      // plain prefill batch keeps the natural order and saves this round.)
+      const int lane = threadIdx.x & 63;
+      const int cpair = x + 8 * min(lane, kp - 1);
+      const SeqData c = seq_data(p, cpair / ngroups, (cpair % ngroups) * group + w % group);
+      j = pair_by_length(lane < kp ? c.kv_len : -1, kp, j);
+      kv_len_pre = __builtin_amdgcn_readlane(c.kv_len, j);
+      hk_pre = __builtin_amdgcn_readlane(c.hk, j);
+      qo_pre = __builtin_amdgcn_readlane(c.qo, j);
+      ko_pre = __builtin_amdgcn_readlane(c.ko, j);
+      pre = true;
+    }
     pair = x + 8 * j;
     qt = ntq - 1 - r;
     head = w % group;
@@ -549,20 +649,35 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const int qrow = q0 + wave * 32 + col;
   f16* op = reinterpret_cast<f16*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
 
-  const int hk = p.kv_head(hq);
-  if (hk < 0) {
-    if (qrow < p.M) {
-      for (int d = half_id * (D / 2); d < (half_id + 1) * (D / 2); ++d)
-        op[(int64_t)qrow * D + d] = (f16)__builtin_nanf("");
-    }
-    return;
+  // The loads that need only (b, hq) leave first, together with the scalar
+  // loads of the key count, head map entry and offsets: Q (rows past M read
+  // row M-1 and are zeroed after the load) and the page rows of the first 64
+  // tiles. No branch separates them from their uses, so the compiler keeps
+  // them here; a head-map entry outside [0, Hk) runs no tiles and writes NaN
+  // rows through the common epilogue.
+  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const int64_t qoff = (int64_t)min(qrow, p.M - 1) * D + 8 * half_id;
+  half8 qreg[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    const half8 v = *reinterpret_cast<const half8*>(qp + qoff + 16 * ks);
+    qreg[ks] = qrow < p.M ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
+  using Table = SlabTable<D, NW, BN>;
+  const typename Table::RowReq req0 = Table::row_load(p, b, lane, wave);
+  const SeqData sd = seq_data(p, b, hq);
+  const int hk = pre ? hk_pre : sd.hk;
+  const int kv_len = pre ? kv_len_pre : sd.kv_len;
+  const int qo = pre ? qo_pre : sd.qo;
+  const int ko = pre ? ko_pre : sd.ko;
+  const bool head_ok = hk >= 0;
+  Table pages;
+  pages.base = 0;
+  pages.rows = Table::row_finish(p, b, req0);
+  pages.hk_rows = head_ok ? (uint32_t)((int64_t)hk * (p.kv.stride_hk / D)) : 0u;
 
-  const int kv_len = p.kv_len(b);
-  const int qo = p.q_off(b);
-  const int ko = p.k_off(b);
   const int last_row = min(q0 + kBM, p.M) - 1;
-  const int wg_lim = row_key_limit(kv_len, p.causal, qo, ko, last_row);
+  const int wg_lim = head_ok ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
   const int ntiles = (wg_lim + BN - 1) / BN;
   const int wrow0 = q0 + wave * 32;
   const int wrow1 = min(wrow0 + 31, p.M - 1);
@@ -574,23 +689,13 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const char* kp = reinterpret_cast<const char*>(p.k);
   const char* vp = reinterpret_cast<const char*>(p.v);
   const SlabLane<D, NW, BN> dl = slab_lane<D, NW, BN>(wave, lane);
-  SlabTable<D, NW, BN> pages;
-  pages.fill(p, b, hk, kv_len, wave, lane, 0);
   if (ntiles > 0) {
-    const QuarterSrc s0 = pages.get(p, b, hk, 0, kv_len, wave, lane);
+    const QuarterSrc s0 = pages.get(p, b, 0, kv_len, wave, lane);
     dma_slab<D, NW, BN>(s0, dl.vk, kp, wave, smem);
     dma_slab<D, NW, BN>(s0, dl.vv, vp, wave, smem + TILE);
   }
-  QuarterSrc next_src = pages.get(p, b, hk, 1, kv_len, wave, lane);
+  QuarterSrc next_src = pages.get(p, b, 1, kv_len, wave, lane);
 
-  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
-  half8 qreg[KSTEPS];
-#pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    qreg[ks] = qrow < p.M
-                   ? *reinterpret_cast<const half8*>(qp + (int64_t)qrow * D + 16 * ks + 8 * half_id)
-                   : half8{0, 0, 0, 0, 0, 0, 0, 0};
-  }
   if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
   // LDS byte offsets of the lane's operands. K: row col, logical chunk
@@ -624,7 +729,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       char* nbuf = smem + (PB ^ 1) * 2 * TILE;
       dma_slab<D, NW, BN>(next_src, dl.vk, kp, wave, nbuf);
       dma_slab<D, NW, BN>(next_src, dl.vv, vp, wave, nbuf + TILE);
-      if (t + 2 < ntiles) next_src = pages.get(p, b, hk, t + 2, kv_len, wave, lane);
+      if (t + 2 < ntiles) next_src = pages.get(p, b, t + 2, kv_len, wave, lane);
     }
     if (k0 >= wave_lim_max) return;
     const char* buf = smem + PB * 2 * TILE;
@@ -711,7 +816,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // Lane (col, half) holds d = 32i + 8g + 4*half + 0..3 of its row, i.e.
   // half of 16-byte chunk 4i + g.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
+  const float inv = !head_ok ? __builtin_nanf("") : kv_len == 0 ? 0.f : 1.f / l_tot;
   __syncthreads();  // every wave has finished reading the last K/V stage
   const int lrow = wave * 32 + col;
 #pragma unroll
