@@ -191,6 +191,27 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
     return out
 
 
+def bench_gemm_reference(dev, n=8192, iters=20):
+    """fp16 GEMM of the vendor library (torch.matmul -> hipBLASLt) on the same
+    GPU: the MFMA rate a plain GEMM sustains here, next to the published peak
+    that roofline.peak uses. Reported only; not part of the attention path."""
+    a = torch.randn(n, n, device=dev, dtype=torch.float16)
+    b = torch.randn(n, n, device=dev, dtype=torch.float16)
+    for _ in range(3):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    tf = 2.0 * n ** 3 / ms / 1e9
+    return {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_MFMA_F16_TFLOPS, 4), "ms": round(ms, 4),
+            "shape": f"{n}x{n}x{n} fp16, fp32 accumulate", "library": "torch.matmul (hipBLASLt)"}
+
+
 def bench_cfg1(steps, warmup, dev):
     res = {}
     for dt in (torch.float16, torch.float32):
@@ -328,7 +349,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="2,4,3,5,1,tm")
+    ap.add_argument("--configs", default="2,4,3,5,1,tm,gemm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-mebibyte device buffer --steps times (the reference "
@@ -402,6 +423,9 @@ def main():
         del w5
     if "1" in cfgs:
         extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
+    if "gemm" in cfgs:
+        extra["fp16_gemm_reference"] = bench_gemm_reference(dev)
+        log(f"fp16 GEMM reference: {extra['fp16_gemm_reference']['tflops']} TFLOP/s")
     if "tm" in cfgs:
         extra["int8_engine_decode_token_major"] = bench_token_major(K, W, dev)
         log(f"token-major decode: "
@@ -413,7 +437,10 @@ def main():
         if key is not None:
             result = extra.pop(key)
         else:
-            key = next(k for k, v in extra.items() if "roofline" in v)
+            key = next((k for k, v in extra.items() if "roofline" in v), None)
+            if key is None:
+                print(json.dumps({"error": "no attention configuration requested", "extra": extra}))
+                sys.exit(2)
             result = dict(extra.pop(key))
             result["value"] = result["roofline"]["achieved"]
             result["unit"] = result["roofline"]["unit"]
