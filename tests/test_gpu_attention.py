@@ -207,6 +207,28 @@ def test_ragged_lengths_every_head(gpu, B, Hq, Hk, M, seed):
     _run_and_check(c, f"ragged B={B} Hq={Hq} Hk={Hk}")
 
 
+@pytest.mark.parametrize("D,causal", [(128, False), (64, True), (64, False)])
+def test_ragged_lengths_without_offsets(gpu, D, causal):
+    """Prompts of different lengths in one prefill batch, no per-sequence
+    offsets: the pairs spread over the XCDs in index order (2 pairs per XCD),
+    every head of every sequence checked, with the rows past each sequence's
+    length masked by causality or by its key count."""
+    lengths = [200, 37, 256, 129, 1, 250, 64, 180]
+    c = _small_paged(8, 16, 2, 256, lengths, D=D, seed=90 + D, causal=causal)
+    _run_and_check(c, f"ragged D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("B,Hq,Hk", [(16, 8, 1), (8, 32, 8)])
+def test_ragged_lengths_d64_sorted(gpu, B, Hq, Hk):
+    """Chunked prefill at D=64 with per-sequence offsets (pairs ordered by
+    length on each XCD)."""
+    g = torch.Generator().manual_seed(95 + B)
+    prior = torch.randint(0, 500, (B,), generator=g).tolist()
+    lengths = [p + 96 for p in prior]
+    c = _small_paged(B, Hq, Hk, 96, lengths, D=64, seed=96 + B, q_offsets=prior)
+    _run_and_check(c, f"ragged D=64 B={B} Hq={Hq} Hk={Hk}")
+
+
 def test_chunked_prefill_per_sequence_offsets(gpu):
     prior = [0, 37, 150, 600]
     M = 130
