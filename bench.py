@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention path on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1,tm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1,tm,gemm]
                     [--no-cpu-baseline]
 
 Prints ONE JSON line on stdout (diagnostics go to stderr). The headline
@@ -15,8 +15,12 @@ full context; decode GB/s counts live K/V + q/o + block-table bytes.
 Configurations 3, 5 and 1 are reported under "extra".
 
 Per-kernel durations come from HIP events recorded on the stream the kernels
-run on (torch's current stream) around every timed launch; `roofline.achieved`
-is algorithmic work per launch / mean launch duration. The CPU baseline is the
+run on (torch's current stream). `roofline.achieved` is algorithmic work per
+launch / mean launch duration, the mean taken over the timed launches run back
+to back between one event pair (`*_back_to_back`); a second pass with events
+around every launch gives the spread (`kernel_ms`: p10, p90, ...). Before a
+workload's warmup steps, 0.1 s of untimed launches let the shader clock
+settle (see `settle`). The CPU baseline is the
 oracle's restatement of the reference's CPU math path
 (flashattention_custom/ops.py:34-72), timed on the host (kind "port").
 """
@@ -89,6 +93,46 @@ def timed(step, steps, warmup, marks=1):
     return wall, segs
 
 
+SETTLE_S = 0.1
+
+
+def settle(step, seconds=SETTLE_S):
+    """Untimed launches for `seconds` of GPU time before a workload's warmup.
+    From idle, the shader clock first boosts, then drops below its sustained
+    level for some tens of launches, then settles (cfg2: about 193 us, then
+    230-250 us, then 195-205 us per launch). The timed steps measure the
+    settled state that a sustained load runs in."""
+    step(None)  # the first call of a configuration may load code or allocate
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            step(None)
+        torch.cuda.synchronize()
+
+
+def back_to_back(step, steps, warmup):
+    """Settle, run `step(None)` warmup+steps times with no events between the
+    launches, and time the `steps` launches with one HIP event pair on the
+    launching stream. Events recorded between launches leave a gap of a few
+    microseconds on the GPU's timeline, which per-launch events would count;
+    this is the mean duration the roofline uses. Returns (wall_s, mean_ms)."""
+    stream = torch.cuda.current_stream()
+    settle(step)
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step(None)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, e0.elapsed_time(e1) / steps
+
+
 def dist(durs):
     """Summary of per-step kernel times in ms: mean, median, p10, p90, min, max."""
     v = sorted(durs)
@@ -126,12 +170,13 @@ def bench_prefill(w, steps, warmup, traffic_key, traffic):
         if ev:
             ev[1].record(stream)
 
-    wall, segs = timed(step, steps, warmup)
+    wall, mean_ms = back_to_back(step, steps, warmup)
+    _, segs = timed(step, steps, 0)
     durs = [s[0] for s in segs]
-    mean_ms = statistics.fmean(durs)
     return {
         "value": round(flops * steps / wall / 1e12, 2), "unit": "TFLOP/s",
         "ms_per_step": round(wall / steps * 1e3, 4),
+        "kernel_ms_back_to_back": round(mean_ms, 4),
         "kernel_ms": dist(durs),
         "flops_per_step": flops,
         "roofline": roofline("mfma", flops, mean_ms, traffic.get(traffic_key)),
@@ -150,12 +195,12 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
     stream = torch.cuda.current_stream()
     it = [0]
 
-    def step(ev):
+    def step(ev, append=True):
         x = pools[it[0] % len(pools)]
         it[0] += 1
         if ev:
             ev[0].record(stream)
-        if x.k_new is not None:
+        if append and x.k_new is not None:
             paged_kv_append(x.k_pool, x.v_pool, x.k_new, x.v_new, x.append_pos, 16,
                             block_table=x.block_table, rope=rope)
         if ev:
@@ -166,15 +211,21 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
         if ev:
             ev[2].record(stream)
 
-    wall, segs = timed(step, steps, warmup, marks=2)
+    # whole steps back to back (the wall clock of `value`), then the decode
+    # alone back to back (its mean is the roofline's; the append rewrites the
+    # same token every step, so the cache is the same either way), then
+    # per-step events for the distributions
+    wall, mean_step = back_to_back(step, steps, warmup)
+    _, mean_dec = back_to_back(lambda ev: step(ev, append=False), steps, 0)
+    _, segs = timed(step, steps, 0, marks=2)
     dec = [s[1] for s in segs]
     app = [s[0] for s in segs]
-    mean_dec = statistics.fmean(dec)
     out = {
         "value": round(nbytes * steps / wall / 1e9, 2) if abytes == 0 else
         round((nbytes + abytes) * steps / wall / 1e9, 2),
         "unit": "GB/s",
         "ms_per_step": round(wall / steps * 1e3, 4),
+        "decode_kernel_ms_back_to_back": round(mean_dec, 4),
         "decode_kernel_ms": dist(dec),
         "decode_bytes_per_step": nbytes,
         "roofline": roofline("hbm", nbytes, mean_dec, traffic.get(traffic_key)),
@@ -187,7 +238,7 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
         out["append_kernel_ms"] = dist(app)
         out["append"] = roofline("hbm", abytes, mean_app, traffic.get("append"))
         out["append_bytes_per_step"] = abytes
-        out["end_to_end_ms"] = round(statistics.fmean([a + d for a, d in zip(app, dec)]), 4)
+        out["end_to_end_ms"] = round(mean_step, 4)
     return out
 
 
@@ -259,10 +310,11 @@ def bench_token_major(steps, warmup, dev, H=40, KVH=8, Dh=128, t=32767, sets=3):
         if ev:
             ev[1].record(stream)
 
-    wall, segs = timed(step, steps, warmup)
+    _, mean_ms = back_to_back(step, steps, warmup)
+    _, segs = timed(step, steps, 0)
     durs = [s[0] for s in segs]
-    return {"kernel_ms": dist(durs), "bytes_per_step": nbytes,
-            "roofline": roofline("hbm", nbytes, statistics.fmean(durs)),
+    return {"kernel_ms_back_to_back": round(mean_ms, 4), "kernel_ms": dist(durs),
+            "bytes_per_step": nbytes, "roofline": roofline("hbm", nbytes, mean_ms),
             "workload": {"heads": H, "kv_heads": KVH, "head_dim": Dh, "t": t,
                          "layout": "token-major [T, KVH, Dh] fp16, fp32 q/out"}}
 
@@ -463,6 +515,7 @@ def main():
                    **result.get("workload", {})},
         "roofline": result["roofline"],
         "cpu_baseline": cpu.get("cfg2"),
+        "kernel_ms_back_to_back": result.get("kernel_ms_back_to_back"),
         "kernel_ms": result.get("kernel_ms"),
     }
     if decode is not None:
