@@ -752,7 +752,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       __builtin_amdgcn_sched_barrier(0);
     }
     constexpr int NMF = 2 * DBLK;
-    constexpr int VA = 3;
+    constexpr int VA = 4;  // V operands read ahead (4: +1.2 % on cfg2 over 3; 5 and 6 no better)
     half8 va[VA];
 #pragma unroll
     for (int m = 0; m < VA; ++m) va[m] = ld_vt<D>(buf, voff, m / DBLK, m % DBLK);
