@@ -229,6 +229,22 @@ def test_ragged_lengths_d64_sorted(gpu, B, Hq, Hk):
     _run_and_check(c, f"ragged D=64 B={B} Hq={Hq} Hk={Hk}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_page_size_128_block_table(gpu, D):
+    """The reference engine's default page size (engine/llama_tp.py:29) over a
+    permuted pool: chunked prefill with per-sequence offsets (ordered by
+    length per XCD) and ragged single-token decode, every head checked."""
+    g = torch.Generator().manual_seed(97 + D)
+    prior = torch.randint(0, 900, (8,), generator=g).tolist()
+    M = 100
+    c = _small_paged(8, 16, 2, M, [p + M for p in prior], PS=128, D=D, seed=98 + D,
+                     q_offsets=prior)
+    _run_and_check(c, f"PS=128 prefill D={D}")
+    lengths = torch.randint(1, 1500, (8,), generator=g).tolist()
+    c = _small_paged(8, 16, 2, 1, lengths, PS=128, D=D, seed=99 + D, causal=False)
+    _run_and_check(c, f"PS=128 decode D={D}")
+
+
 def test_chunked_prefill_per_sequence_offsets(gpu):
     prior = [0, 37, 150, 600]
     M = 130
