@@ -200,6 +200,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
     p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
     p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
     p.dec_wgs = fa::decode_launch_wgs(plan, D, PS % 16 == 0);
+    p.dec_seg_cost = PS % 16 == 0 ? fa::kSegmentCost : 0;
     p.dec_rows = plan.rows;
     return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
   }
@@ -331,6 +332,7 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
   p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
   p.dec_wgs = fa::decode_launch_wgs(plan, Dh, false);  // strided rows: per-row loads
+  p.dec_seg_cost = 0;  // one workgroup per CU: a segment start costs little
   p.dec_rows = plan.rows;
   return launch_status(fa::launch_decode(p, Dh, (hipStream_t)stream));
 }

@@ -104,6 +104,7 @@ struct AttnParams {
   float* ws_ml;         // [B*Hk + dec_wgs, dec_rows, 2]  (log2 max, sum)
   int* ws_units;        // [B + 1] units (16-key groups x Hk) before sequence b
   int dec_wgs;          // workgroups of the decode kernel
+  int dec_seg_cost;     // units charged per segment start in the decode split (fa_decode.hip)
   int dec_rows;         // row capacity of a slot: Hq * M
   // optional rotary embedding of Q at load time (nullptr: none): fp16 tables
   // [rope_len, D/2]; query row i of sequence b sits at position q_off(b) + i
@@ -191,6 +192,10 @@ struct DecodePlan {
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
 // Workgroups to launch for a plan on the current device (<= plan.wgs).
 int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned);
+// Units a segment start is charged in the paged decode split: the dependent
+// chain that opens a (sequence, KV head) segment, measured in streamed units
+// with two decode workgroups per CU.
+constexpr int kSegmentCost = 8;
 bool use_decode_path(int B, int M, int Hq, int Hk);
 
 }  // namespace fa

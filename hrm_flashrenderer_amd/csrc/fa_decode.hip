@@ -204,9 +204,48 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
   __syncthreads();
 }
 
+// Cost split of the unit list. A workgroup that starts a (b, hk) segment
+// pays a dependent chain (key count, head scan, Q, page lookup, first K/V);
+// with two workgroups per CU contending for memory, that takes about as long
+// as streaming kSegmentCost units (p.dec_seg_cost; 0 for the one-per-CU
+// per-row variant). Unit u costs u + P * seg(u), seg(u) = b * Hk + hk being
+// its segment's index (empty segments included), and workgroup w owns the
+// units whose cost lies in [floor(w * C / W), floor((w + 1) * C / W)),
+// C = U + P * B * Hk. With P = 0 this is the plain equal split of units; P is
+// 0 unless there are at least 2W units, so that every workgroup's cost range
+// holds two or more costs. Measured against the equal split: cfg3 +3-7 %,
+// cfg4 +1-2 %.
+__device__ __forceinline__ int split_cost_p(const AttnParams& p, int U, int W) {
+  return U >= 2 * W ? min(p.dec_seg_cost, U / (2 * W)) : 0;
+}
+
+// Smallest unit u whose cost is at least floor(w * C / W); U for w == W.
+__device__ __forceinline__ int split_start(const int* units, int B, int Hk, int U, int W, int P,
+                                           int w) {
+  const int64_t C = (int64_t)U + (int64_t)P * B * Hk;
+  const int64_t T = (int64_t)w * C / W;
+  if (T >= C) return U;
+  if (P == 0) return (int)T;
+  // last segment j with cost(start of j) <= T
+  int lo = 0, hi = B * Hk - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    const int b = mid / Hk, hk = mid - b * Hk;
+    const int G = (units[b + 1] - units[b]) / Hk;
+    const int64_t start = (int64_t)units[b] + (int64_t)hk * G;
+    if (start + (int64_t)P * mid <= T) lo = mid; else hi = mid - 1;
+  }
+  const int b = lo / Hk, hk = lo - b * Hk;
+  const int G = (units[b + 1] - units[b]) / Hk;
+  const int64_t start = (int64_t)units[b] + (int64_t)hk * G;
+  const int64_t u = T - (int64_t)P * lo;
+  return (int)min(max(u, start), start + G);
+}
+
 // Balanced decode. The work is the list of units (sequence b, KV head hk,
-// 16-key group g) in (b, hk, g) order; workgroup w of W takes units
-// [w*U/W, (w+1)*U/W), i.e. an equal share whatever the sequence lengths. It
+// 16-key group g) in (b, hk, g) order; workgroup w of W takes a contiguous
+// range of it under the cost split above (an equal share of units plus
+// segment starts, whatever the sequence lengths). It
 // walks the (b, hk) segments of its range; for each it runs all query rows
 // of hk over its groups and writes one partial (max, sum, O) per row at slot
 // b*Hk + hk + w. Along the unit list both the segment and the workgroup
@@ -243,8 +282,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   if (w == 0) {
     for (int b = tid; b <= p.B; b += kDecodeThreads) p.ws_units[b] = s_units[b];
   }
-  const int u0 = (int)((int64_t)w * U / W);
-  const int u1 = (int)((int64_t)(w + 1) * U / W);
+  const int P = split_cost_p(p, U, W);
+  const int u0 = split_start(s_units, p.B, p.Hk, U, W, P, w);
+  const int u1 = split_start(s_units, p.B, p.Hk, U, W, P, w + 1);
   if (u0 >= u1) return;
 
   const f16* qp = reinterpret_cast<const f16*>(p.q);
@@ -525,9 +565,13 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     float acc[DPW];
 #pragma unroll
     for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
+    // workgroups owning the segment's units under the decode kernel's cost split
+    const int P = split_cost_p(p, U, W);
+    const int64_t C = (int64_t)U + (int64_t)P * p.B * p.Hk;
+    const int64_t seg_cost = (int64_t)P * (b * p.Hk + hk);
     if (G > 0) {
-      const int wa = (int)min((int64_t)W - 1, ((int64_t)(US + 1) * W - 1) / U);
-      const int wb = (int)min((int64_t)W - 1, ((int64_t)UE * W - 1) / U);
+      const int wa = (int)min((int64_t)W - 1, ((US + seg_cost + 1) * W - 1) / C);
+      const int wb = (int)min((int64_t)W - 1, ((UE + seg_cost) * W - 1) / C);
       const int first = WIDE ? wa + wave : wa;
       constexpr int STEP = WIDE ? 4 : 1;
       // Slots in batches of 4 with every load issued before the merge; slots
@@ -538,7 +582,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
           const int w = w0 + i * STEP;
-          const bool live = w <= wb && (int64_t)w * U / W != (int64_t)(w + 1) * U / W;
+          const bool live = w <= wb && (int64_t)w * C / W != (int64_t)(w + 1) * C / W;
           const int64_t srow = rbase + (int64_t)w * p.dec_rows;
           pm[i] = live ? p.ws_ml[srow * 2] : -INFINITY;
           pl[i] = live ? p.ws_ml[srow * 2 + 1] : 0.f;
