@@ -194,8 +194,9 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens)
 int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned);
 // Units a segment start is charged in the paged decode split: the dependent
 // chain that opens a (sequence, KV head) segment, measured in streamed units
-// with two decode workgroups per CU.
-constexpr int kSegmentCost = 8;
+// with two decode workgroups per CU (a sweep of 0-32 peaks at 12-16 for both
+// benchmark decode shapes).
+constexpr int kSegmentCost = 12;
 bool use_decode_path(int B, int M, int Hq, int Hk);
 
 }  // namespace fa

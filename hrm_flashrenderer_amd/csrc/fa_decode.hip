@@ -213,8 +213,8 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
 // units whose cost lies in [floor(w * C / W), floor((w + 1) * C / W)),
 // C = U + P * B * Hk. With P = 0 this is the plain equal split of units; P is
 // 0 unless there are at least 2W units, so that every workgroup's cost range
-// holds two or more costs. Measured against the equal split: cfg3 +3-7 %,
-// cfg4 +1-2 %.
+// holds two or more costs. Measured against the equal split: cfg3 +5 %,
+// cfg4 +1.5 %.
 __device__ __forceinline__ int split_cost_p(const AttnParams& p, int U, int W) {
   return U >= 2 * W ? min(p.dec_seg_cost, U / (2 * W)) : 0;
 }

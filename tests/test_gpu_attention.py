@@ -272,6 +272,21 @@ def test_decode_combine_modes(gpu, B, Hq, Hk, seed):
     _run_and_check(c, f"decode rows={B * Hq}")
 
 
+@pytest.mark.parametrize("lengths", [[0, 0, 9000, 0, 1, 0, 4000, 0, 15, 0],
+                                     [0] * 30 + [20000] + [0] * 30 + [17, 0]])
+def test_decode_cost_split_empty_segments(gpu, lengths):
+    """The decode split charges every (sequence, KV head) segment, empty ones
+    included, a fixed number of units once there are at least two units per
+    workgroup (here 6000-10000 units over 512 workgroups): empty sequences
+    around and between long ones must leave every row's slots where the
+    combine kernel looks for them, and rows with no keys come out as zeros."""
+    c = _small_paged(len(lengths), 40, 8, 1, lengths, seed=34, causal=False)
+    out = _run_and_check(c, f"decode B={len(lengths)} with empty sequences")
+    for b, n in enumerate(lengths):
+        if n == 0:
+            assert (out[b] == 0).all(), f"sequence {b} has no keys"
+
+
 @pytest.mark.parametrize("M,causal", [(2, True), (3, False), (4, True), (16, True)])
 def test_decode_few_rows(gpu, M, causal):
     lengths = [400, 1500, 33]
