@@ -285,7 +285,7 @@ def bench_cfg1(steps, warmup, dev):
     return res
 
 
-def bench_token_major(steps, warmup, dev, H=40, KVH=8, Dh=128, t=32767, sets=3):
+def bench_token_major(steps, warmup, dev, traffic, H=40, KVH=8, Dh=128, t=32767, sets=3):
     """The INT8 engine's decode step (batch 1, token-major fp16 cache, fp32 q and
     out) at the Qwen-32B head counts and a 32K context, rotating `sets` caches
     (3 x 134 MB of K and V) so the step reads HBM, not the 256 MB MALL."""
@@ -314,7 +314,7 @@ def bench_token_major(steps, warmup, dev, H=40, KVH=8, Dh=128, t=32767, sets=3):
     _, segs = timed(step, steps, 0)
     durs = [s[0] for s in segs]
     return {"kernel_ms_back_to_back": round(mean_ms, 4), "kernel_ms": dist(durs),
-            "bytes_per_step": nbytes, "roofline": roofline("hbm", nbytes, mean_ms),
+            "bytes_per_step": nbytes, "roofline": roofline("hbm", nbytes, mean_ms, traffic.get("decode_token_major")),
             "workload": {"heads": H, "kv_heads": KVH, "head_dim": Dh, "t": t,
                          "layout": "token-major [T, KVH, Dh] fp16, fp32 q/out"}}
 
@@ -479,7 +479,7 @@ def main():
         extra["fp16_gemm_reference"] = bench_gemm_reference(dev)
         log(f"fp16 GEMM reference: {extra['fp16_gemm_reference']['tflops']} TFLOP/s")
     if "tm" in cfgs:
-        extra["int8_engine_decode_token_major"] = bench_token_major(K, W, dev)
+        extra["int8_engine_decode_token_major"] = bench_token_major(K, W, dev, traffic)
         log(f"token-major decode: "
             f"{extra['int8_engine_decode_token_major']['roofline']['achieved']} GB/s")
     torch.cuda.synchronize()
