@@ -287,6 +287,26 @@ def test_decode_cost_split_empty_segments(gpu, lengths):
             assert (out[b] == 0).all(), f"sequence {b} has no keys"
 
 
+@pytest.mark.parametrize("length", [2032, 2048, 2049, 4112])
+def test_decode_cost_split_thresholds(gpu, length):
+    """One sequence, 8 KV heads: 8 * ceil(length / 16) units = 1016, 1024,
+    1032 and 2056, on either side of the two-units-per-workgroup threshold
+    (1024 with 512 workgroups) where the segment charge switches on, and
+    where it is capped at units / (2 * workgroups)."""
+    c = _small_paged(1, 64, 8, 1, [length], seed=35, causal=False)
+    _run_and_check(c, f"decode length={length}")
+
+
+@pytest.mark.parametrize("seed", [36, 37])
+def test_decode_d64_ragged(gpu, seed):
+    """Head size 64 through the decode kernels with segment charges on
+    (about 6000 units over the device's workgroups)."""
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(0, 3000, (8,), generator=g).tolist()
+    c = _small_paged(8, 64, 8, 1, lengths, D=64, seed=seed, causal=False)
+    _run_and_check(c, f"decode D=64 lengths={lengths}")
+
+
 @pytest.mark.parametrize("M,causal", [(2, True), (3, False), (4, True), (16, True)])
 def test_decode_few_rows(gpu, M, causal):
     lengths = [400, 1500, 33]
