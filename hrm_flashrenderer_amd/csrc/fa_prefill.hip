@@ -853,23 +853,44 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
 }
 
 // fp32 contiguous attention (the reference's CPU path accepts fp32,
-// flashattention_custom/ops.py:19-31). Exact fp32 arithmetic on the vector
-// ALUs: one wave of 64 query rows per workgroup, Q rows in LDS, K/V streamed
-// in 16-key tiles.
+// flashattention_custom/ops.py:19-31), in fp32 arithmetic on the vector ALUs.
+// A workgroup takes kF32Rows query rows of one (sequence, q head). Within a
+// wave, the four lanes of a row split the head dimension (lane = 4 * row +
+// part) and sum their partial dot products with two lane exchanges, so all
+// four hold the same score. The eight waves split every LDS tile of 4096/D
+// keys (8 keys each at D = 64, 4 at D = 128), and each keeps its own online
+// softmax state; the eight states are merged in LDS at the end. So a row's
+// keys run on 32 lanes at once (the causal rows at the end of a sequence set
+// the kernel's duration), and a 512-row head spreads over 32 workgroups. The
+// next tile's K and V rows are loaded into registers while the current tile
+// is computed (8 + 8 floats per thread).
+constexpr int kF32Rows = 16;
+constexpr int kF32Waves = 8;
+
 template <int D>
-__global__ __launch_bounds__(64) void prefill_f32_kernel(AttnParams p) {
-  constexpr int BN = 16;
-  __shared__ float sQ[64][D + 1];
+__global__ __launch_bounds__(64 * kF32Waves) void prefill_f32_kernel(AttnParams p) {
+  constexpr int BN = 4096 / D;    // keys per LDS tile
+  constexpr int NW = kF32Waves;
+  constexpr int NT = 64 * NW;
+  constexpr int KPW = BN / NW;    // keys per wave and tile
+  constexpr int EPT = BN * D / NT;  // K (and V) elements per thread and tile
+  constexpr int DP = D / 4;       // head dims per lane
   __shared__ float sK[BN][D];
   __shared__ float sV[BN][D];
-  const int qt = blockIdx.x;
+  __shared__ float sM[NW][kF32Rows];
+  __shared__ float sL[NW][kF32Rows];
+  __shared__ float sO[NW][kF32Rows][D + 1];  // +1: the 16 rows x 4 parts hit 64 banks
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane >> 2;
+  const int part = lane & 3;
+  const int q0 = blockIdx.x * kF32Rows;
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
-  const int lane = threadIdx.x;
-  const int q0 = qt * 64;
-  const int qrow = q0 + lane;
-  float* op = reinterpret_cast<float*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const int qrow = q0 + r;
   const float* qp = reinterpret_cast<const float*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  float* op = reinterpret_cast<float*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
   const float* kp = reinterpret_cast<const float*>(p.k);
   const float* vp = reinterpret_cast<const float*>(p.v);
   const int hk = p.kv_head(hq);
@@ -877,76 +898,122 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(AttnParams p) {
   const int qo = p.q_off(b);
   const int ko = p.k_off(b);
 
-  for (int e = lane; e < 64 * D; e += 64) {
-    const int r = e / D, d = e % D;
-    sQ[r][d] = (q0 + r < p.M) ? qp[(int64_t)(q0 + r) * D + d] : 0.f;
-  }
-  const int last_row = min(q0 + 64, p.M) - 1;
+  float q[DP];
+#pragma unroll
+  for (int i = 0; i < DP; ++i) q[i] = qrow < p.M ? qp[(int64_t)qrow * D + part * DP + i] : 0.f;
+  const int last_row = min(q0 + kF32Rows, p.M) - 1;
   const int wg_lim = hk < 0 ? 0 : row_key_limit(kv_len, p.causal, qo, ko, last_row);
   const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
   const float scale = p.scale_log2 / kLog2e;  // 1/sqrt(D)
 
-  float o[D];
+  float o[DP];
 #pragma unroll
-  for (int d = 0; d < D; ++d) o[d] = 0.f;
+  for (int i = 0; i < DP; ++i) o[i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
+  // Element i of a thread's share of a tile is (key row, dim) = divmod(tid +
+  // NT i, D): consecutive threads read consecutive dims of a row.
+  float nk[EPT], nv[EPT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + NT * i;
+      const int j = k0 + e / D;
+      const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
+      nk[i] = off >= 0 ? kp[off + e % D] : 0.f;
+      nv[i] = off >= 0 ? vp[off + e % D] : 0.f;
+    }
+  };
+  if (wg_lim > 0) fetch(0);
   for (int k0 = 0; k0 < wg_lim; k0 += BN) {
     __syncthreads();
-    for (int e = lane; e < BN * D; e += 64) {
-      const int r = e / D, d = e % D;
-      const int j = k0 + r;
-      const int64_t off = j < kv_len ? p.kv.row_offset(b, hk, j) : -1;
-      sK[r][d] = off >= 0 ? kp[off + d] : 0.f;
-      sV[r][d] = off >= 0 ? vp[off + d] : 0.f;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + NT * i;
+      sK[e / D][e % D] = nk[i];
+      sV[e / D][e % D] = nv[i];
     }
     __syncthreads();
-    float s[BN];
+    if (k0 + BN < wg_lim) fetch(k0 + BN);
+    float s[KPW];
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < BN; ++r) {
+    for (int i = 0; i < KPW; ++i) {
+      const int kr = wave * KPW + i;
       float acc = 0.f;
-#pragma unroll 16
-      for (int d = 0; d < D; ++d) acc = __builtin_fmaf(sQ[lane][d], sK[r][d], acc);
-      s[r] = (k0 + r < lim) ? acc * scale : -INFINITY;
-      mx = fmaxf(mx, s[r]);
+#pragma unroll
+      for (int d = 0; d < DP; ++d) acc = __builtin_fmaf(q[d], sK[kr][part * DP + d], acc);
+      // a + b == b + a exactly, so the four lanes of the row agree bit for bit
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      s[i] = (k0 + kr < lim) ? acc * scale : -INFINITY;
+      mx = fmaxf(mx, s[i]);
     }
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = expf(m_run - m_use);
     float psum = 0.f;
 #pragma unroll
-    for (int r = 0; r < BN; ++r) {
-      s[r] = expf(s[r] - m_use);
-      psum += s[r];
+    for (int i = 0; i < KPW; ++i) {
+      s[i] = expf(s[i] - m_use);
+      psum += s[i];
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
+    for (int d = 0; d < DP; ++d) {
       float acc = o[d] * alpha;
 #pragma unroll
-      for (int r = 0; r < BN; ++r) acc = __builtin_fmaf(s[r], sV[r][d], acc);
+      for (int i = 0; i < KPW; ++i) acc = __builtin_fmaf(s[i], sV[wave * KPW + i][part * DP + d], acc);
       o[d] = acc;
     }
   }
-  if (qrow >= p.M) return;
-  float inv;
-  if (hk < 0) inv = __builtin_nanf("");
-  else inv = kv_len == 0 ? 0.f : 1.f / l_run;
+
+  // Merge the waves' states per row, then write O (consecutive threads,
+  // consecutive dims).
+  if (part == 0) {
+    sM[wave][r] = m_run;
+    sL[wave][r] = l_run;
+  }
 #pragma unroll
-  for (int d = 0; d < D; ++d) op[(int64_t)qrow * D + d] = o[d] * inv;
+  for (int d = 0; d < DP; ++d) sO[wave][r][part * DP + d] = o[d];
+  __syncthreads();
+  for (int e = tid; e < kF32Rows * D; e += NT) {
+    const int row = e / D, d = e % D;
+    if (q0 + row >= p.M) break;
+    float val;
+    if (hk < 0) {
+      val = __builtin_nanf("");
+    } else if (kv_len == 0) {
+      val = 0.f;  // no keys: zeros (flashattention_custom/ops.py:39, 52-59 with slen == 0)
+    } else {
+      float m_all = sM[0][row];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) m_all = fmaxf(m_all, sM[w][row]);
+      float l = 0.f, acc = 0.f;
+      if (m_all != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float c = expf(sM[w][row] - m_all);  // a wave with no visible key: 0
+          l += c * sL[w][row];
+          acc += c * sO[w][row][d];
+        }
+      }
+      val = acc * (1.f / l);  // no visible key: 0 * inf = NaN, the fully masked row
+    }
+    op[(int64_t)(q0 + row) * D + d] = val;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream) {
   if (dtype == 1) {
-    const dim3 grid((unsigned)((p.M + 63) / 64), (unsigned)p.Hq, (unsigned)p.B);
+    const dim3 grid((unsigned)((p.M + kF32Rows - 1) / kF32Rows), (unsigned)p.Hq, (unsigned)p.B);
     if (D == 128)
-      hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(64 * kF32Waves), 0, stream, p);
     else
-      hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(64), 0, stream, p);
+      hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(64 * kF32Waves), 0, stream, p);
     return hipGetLastError();
   }
   const bool aligned = p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D;
