@@ -4,9 +4,9 @@ Exports the reference's three operators (flashattention_custom/__init__.py:1-3)
 backed by hand-written HIP kernels in libfa_mi355x.so, and a shared-pool
 paged K/V cache (the caller-side cache of engine/llama_tp.py:21-107).
 """
-from .ops import flash_attn, flash_attn_paged, paged_kv_append
-from .kv_cache import PagedKVCache, chunked_prefill_plan
+from .ops import flash_attn, flash_attn_paged, paged_kv_append, paged_kv_scatter
+from .kv_cache import PagedKVCache, chunked_prefill_plan, chunked_prefill_schedule
 from .rope import build_rope_cache
 
-__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append", "PagedKVCache",
-           "build_rope_cache", "chunked_prefill_plan"]
+__all__ = ["flash_attn", "flash_attn_paged", "paged_kv_append", "paged_kv_scatter", "PagedKVCache",
+           "build_rope_cache", "chunked_prefill_plan", "chunked_prefill_schedule"]

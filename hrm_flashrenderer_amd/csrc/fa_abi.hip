@@ -152,7 +152,8 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                      const int32_t* seqlen, int page_size, const int32_t* head_map, void* o, int B,
                      int Hq, int M, int D, int NB, int Hk, int P, int causal, int64_t q_offset,
                      int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
-                     const int32_t* block_table, int max_blocks, void* workspace,
+                     const int32_t* q_lens, const int32_t* block_table, int max_blocks,
+                     void* workspace,
                      size_t workspace_bytes, const void* rope_cos, const void* rope_sin,
                      int rope_len, void* stream) {
   if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
@@ -174,6 +175,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
   p.head_map = head_map;
   p.q_offsets = q_offsets;
   p.k_offsets = k_offsets;
+  p.q_lens = q_lens;
   p.kv = paged_map(block_table, max_blocks, NB, Hk, P, PS, D);
   p.B = B;
   p.Hq = Hq;
@@ -199,7 +201,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
     p.ws_o = reinterpret_cast<float*>(ws);
     p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
     p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-    p.dec_wgs = fa::decode_launch_wgs(plan, D, PS % 16 == 0);
+    p.dec_wgs = fa::decode_launch_wgs(plan, p, D);
     p.dec_seg_cost = PS % 16 == 0 ? fa::kSegmentCost : 0;
     p.dec_rows = plan.rows;
     return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
@@ -211,11 +213,12 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
                             const int32_t* seqlen, int page_size, const int32_t* head_map, void* o,
                             int B, int Hq, int M, int D, int NB, int Hk, int P, int causal,
                             int64_t q_offset, int64_t k_offset, const int32_t* q_offsets,
-                            const int32_t* k_offsets, const int32_t* block_table, int max_blocks,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+                            const int32_t* k_offsets, const int32_t* q_lens,
+                            const int32_t* block_table, int max_blocks, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
-                   causal, q_offset, k_offset, q_offsets, k_offsets, block_table, max_blocks,
-                   workspace, workspace_bytes, nullptr, nullptr, 0, stream);
+                   causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
+                   max_blocks, workspace, workspace_bytes, nullptr, nullptr, 0, stream);
 }
 
 int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void* v_pages,
@@ -223,20 +226,22 @@ int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void*
                                  void* o, int B, int Hq, int M, int D, int NB, int Hk, int P,
                                  int causal, int64_t q_offset, int64_t k_offset,
                                  const int32_t* q_offsets, const int32_t* k_offsets,
-                                 const int32_t* block_table, int max_blocks, void* workspace,
-                                 size_t workspace_bytes, const void* rope_cos,
-                                 const void* rope_sin, int rope_len, void* stream) {
+                                 const int32_t* q_lens, const int32_t* block_table,
+                                 int max_blocks, void* workspace, size_t workspace_bytes,
+                                 const void* rope_cos, const void* rope_sin, int rope_len,
+                                 void* stream) {
   if (rope_cos == nullptr || rope_sin == nullptr || rope_len <= 0)
     return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
   return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
-                   causal, q_offset, k_offset, q_offsets, k_offsets, block_table, max_blocks,
-                   workspace, workspace_bytes, rope_cos, rope_sin, rope_len, stream);
+                   causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
+                   max_blocks, workspace, workspace_bytes, rope_cos, rope_sin, rope_len, stream);
 }
 
 static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
                      int Hk, int T, int D, int NB, int P, int page_size, int64_t start_pos,
-                     const int32_t* start_positions, const int32_t* block_table, int max_blocks,
-                     const void* rope_cos, const void* rope_sin, int rope_len, void* stream) {
+                     const int32_t* start_positions, const int32_t* token_positions,
+                     const int32_t* block_table, int max_blocks, const void* rope_cos,
+                     const void* rope_sin, int rope_len, void* stream) {
   if (B < 0 || T < 0 || D <= 0) return fail(FA_ERR_INVALID, "shape mismatch");
   int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
   if (rc != FA_OK) return rc;
@@ -250,7 +255,8 @@ static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void
   (void)hipGetLastError();
   return launch_status(fa::launch_paged_append(
       k_pages, v_pages, k_new, v_new, map, B, Hk, T, narrow(start_pos), start_positions,
-      reinterpret_cast<const fa::f16*>(rope_cos), reinterpret_cast<const fa::f16*>(rope_sin),
+      token_positions, reinterpret_cast<const fa::f16*>(rope_cos),
+      reinterpret_cast<const fa::f16*>(rope_sin),
       rope_len, (hipStream_t)stream));
 }
 
@@ -259,7 +265,7 @@ int fa_paged_kv_append(void* k_pages, void* v_pages, const void* k_new, const vo
                        const int32_t* start_positions, const int32_t* block_table, int max_blocks,
                        void* stream) {
   return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, start_pos,
-                   start_positions, block_table, max_blocks, nullptr, nullptr, 0, stream);
+                   start_positions, nullptr, block_table, max_blocks, nullptr, nullptr, 0, stream);
 }
 
 int fa_paged_kv_append_rope(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
@@ -270,7 +276,20 @@ int fa_paged_kv_append_rope(void* k_pages, void* v_pages, const void* k_new, con
   if (rope_cos == nullptr || rope_sin == nullptr || rope_len <= 0)
     return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
   return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, start_pos,
-                   start_positions, block_table, max_blocks, rope_cos, rope_sin, rope_len, stream);
+                   start_positions, nullptr, block_table, max_blocks, rope_cos, rope_sin, rope_len,
+                   stream);
+}
+
+int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
+                        int Hk, int T, int D, int NB, int P, int page_size,
+                        const int32_t* positions, const int32_t* block_table, int max_blocks,
+                        const void* rope_cos, const void* rope_sin, int rope_len, void* stream) {
+  if (positions == nullptr && (int64_t)B * Hk * T > 0)
+    return fail(FA_ERR_INVALID, "positions [B, T] required");
+  if ((rope_cos == nullptr) != (rope_sin == nullptr) || (rope_cos != nullptr && rope_len <= 0))
+    return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
+  return kv_append(k_pages, v_pages, k_new, v_new, B, Hk, T, D, NB, P, page_size, 0, nullptr,
+                   positions, block_table, max_blocks, rope_cos, rope_sin, rope_len, stream);
 }
 
 size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max) {
@@ -331,7 +350,7 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.ws_o = reinterpret_cast<float*>(ws);
   p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
   p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-  p.dec_wgs = fa::decode_launch_wgs(plan, Dh, false);  // strided rows: per-row loads
+  p.dec_wgs = fa::decode_launch_wgs(plan, p, Dh);  // per-row loads, fp32 query split
   p.dec_seg_cost = 0;  // one workgroup per CU: a segment start costs little
   p.dec_rows = plan.rows;
   return launch_status(fa::launch_decode(p, Dh, (hipStream_t)stream));

@@ -5,6 +5,9 @@
 // (flashattention_custom/ops.py:63-72): token t of sequence b goes to position
 // start + t, i.e. page (start+t)/PS, slot (start+t)%PS, for every KV head.
 // Positions whose page is out of range are skipped (reference :548).
+// With per-token positions ([B, T], the general path of the reference's
+// cache, engine/llama_tp.py:80-99), token t of sequence b goes to
+// positions[b*T + t] instead; negative positions are skipped.
 //
 // Layout of the work: one lane moves one 16-byte chunk (8 fp16) of K and the
 // same chunk of V. Consecutive lanes take consecutive chunks of a token row,
@@ -21,7 +24,8 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
     f16* __restrict__ k_pages, f16* __restrict__ v_pages,
     const f16* __restrict__ k_new, const f16* __restrict__ v_new,
     KVMap map, int B, int Hk, int T, int chunks_per_row, int chunk_shift, int start_pos,
-    const int32_t* __restrict__ start_positions, int64_t total_chunks) {
+    const int32_t* __restrict__ start_positions, const int32_t* __restrict__ token_positions,
+    int64_t total_chunks) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total_chunks) return;
   int chunk;
@@ -38,8 +42,8 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
   const int hk = (int)(bh % Hk);
   const int b = (int)(bh / Hk);
 
-  const int start = start_positions ? start_positions[b] : start_pos;
-  const int pos = start + t;
+  const int pos = token_positions ? token_positions[(int64_t)b * T + t]
+                                  : (start_positions ? start_positions[b] : start_pos) + t;
   if (pos < 0) return;
   const int64_t dst_row = map.row_offset(b, hk, pos);
   if (dst_row < 0) return;
@@ -61,7 +65,8 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
     f16* __restrict__ k_pages, f16* __restrict__ v_pages,
     const f16* __restrict__ k_new, const f16* __restrict__ v_new,
     KVMap map, int B, int Hk, int T, int pairs_per_row, int start_pos,
-    const int32_t* __restrict__ start_positions, const f16* __restrict__ rope_cos,
+    const int32_t* __restrict__ start_positions, const int32_t* __restrict__ token_positions,
+    const f16* __restrict__ rope_cos,
     const f16* __restrict__ rope_sin, int rope_len, int64_t total_pairs) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total_pairs) return;
@@ -72,8 +77,8 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
   const int hk = (int)(bh % Hk);
   const int b = (int)(bh / Hk);
 
-  const int start = start_positions ? start_positions[b] : start_pos;
-  const int pos = start + t;
+  const int pos = token_positions ? token_positions[(int64_t)b * T + t]
+                                  : (start_positions ? start_positions[b] : start_pos) + t;
   if (pos < 0) return;
   const int64_t dst_row = map.row_offset(b, hk, pos);
   if (dst_row < 0) return;
@@ -103,8 +108,9 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
 
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
-                               const int32_t* start_positions, const f16* rope_cos,
-                               const f16* rope_sin, int rope_len, hipStream_t stream) {
+                               const int32_t* start_positions, const int32_t* token_positions,
+                               const f16* rope_cos, const f16* rope_sin, int rope_len,
+                               hipStream_t stream) {
   const int threads = 256;
   if (rope_cos != nullptr) {
     const int pairs_per_row = map.D / 16;
@@ -114,8 +120,8 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
     hipLaunchKernelGGL(paged_append_rope_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
                        reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
                        reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new),
-                       map, B, Hk, T, pairs_per_row, start_pos, start_positions, rope_cos,
-                       rope_sin, rope_len, total);
+                       map, B, Hk, T, pairs_per_row, start_pos, start_positions,
+                       token_positions, rope_cos, rope_sin, rope_len, total);
     return hipGetLastError();
   }
   const int chunks_per_row = map.D / 8;
@@ -128,7 +134,8 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
   hipLaunchKernelGGL(paged_append_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
                      reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
                      reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new), map,
-                     B, Hk, T, chunks_per_row, chunk_shift, start_pos, start_positions, total);
+                     B, Hk, T, chunks_per_row, chunk_shift, start_pos, start_positions,
+                     token_positions, total);
   return hipGetLastError();
 }
 

@@ -92,6 +92,8 @@ struct AttnParams {
   const int32_t* head_map;  // paged: [Hq]; contiguous: nullptr (h / group)
   const int32_t* q_offsets; // nullable [B]
   const int32_t* k_offsets; // nullable [B]
+  const int32_t* q_lens;    // nullable [B]: rows >= q_lens[b] of sequence b are padding
+                            // (not computed; written as zeros)
   KVMap kv;
   int B, Hq, Hk, M, N;  // N: contiguous key count, or per-sequence capacity in tokens
   int group;            // Hq / Hk (contiguous head mapping)
@@ -119,6 +121,12 @@ struct AttnParams {
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
+  // Query rows of sequence b that are not padding, in [0, M].
+  __device__ __forceinline__ int q_len(int b) const {
+    if (q_lens == nullptr) return M;
+    const int n = q_lens[b];
+    return n < 0 ? 0 : n > M ? M : n;
+  }
   // Number of keys of sequence b (clamped to the capacity).
   __device__ __forceinline__ int kv_len(int b) const {
     if (seqlen == nullptr) return N;
@@ -176,8 +184,9 @@ __device__ __forceinline__ void rope_fragment(half8* q, const AttnParams& p, int
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
-                               const int32_t* start_positions, const f16* rope_cos,
-                               const f16* rope_sin, int rope_len, hipStream_t stream);
+                               const int32_t* start_positions, const int32_t* token_positions,
+                               const f16* rope_cos, const f16* rope_sin, int rope_len,
+                               hipStream_t stream);
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream);
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
 
@@ -190,8 +199,9 @@ struct DecodePlan {
   size_t ws_bytes;  // total, including the unit prefix
 };
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
-// Workgroups to launch for a plan on the current device (<= plan.wgs).
-int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned);
+// Workgroups to launch for a plan on the current device (<= plan.wgs), for the
+// decode kernel variant the arguments select.
+int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D);
 // Units a segment start is charged in the paged decode split: the dependent
 // chain that opens a (sequence, KV head) segment, measured in streamed units
 // with two decode workgroups per CU (a sweep of 0-32 peaks at 12-16 for both

@@ -170,10 +170,12 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
 }
 
 // Groups (16 keys) of sequence b that some query row can see.
+// Padding rows (q_lens) see no keys, so a sequence without live rows has none.
 __device__ __forceinline__ int visible_groups(const AttnParams& p, int b) {
-  int kv_lim = p.kv_len(b);
+  const int qlen = p.q_len(b);
+  int kv_lim = qlen > 0 ? p.kv_len(b) : 0;
   if (p.causal) {
-    const int64_t lim = (int64_t)p.q_off(b) + (p.M - 1) - p.k_off(b) + 1;
+    const int64_t lim = (int64_t)p.q_off(b) + (qlen - 1) - p.k_off(b) + 1;
     if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
   }
   return kv_lim > 0 ? (kv_lim + 15) >> 4 : 0;
@@ -251,7 +253,16 @@ __device__ __forceinline__ int split_start(const int* units, int B, int Hk, int 
 // b*Hk + hk + w. Along the unit list both the segment and the workgroup
 // index are non-decreasing and at least one grows at every change, so
 // segment + workgroup is unique per (segment, workgroup) pair.
-template <int D, bool ALIGNED>
+//
+// QSPLIT (fp32 Q, the token-major entry): the engine computes q . k in fp32
+// (scripts/deepseek_native_engine.sh:573-577). Each query row is split into
+// q_hi = fp16(q') and q_lo = fp16(q' - q_hi), q' = q * 2^-e, and S^T takes
+// both through the matrix cores (exact fp16 x fp16 products, fp32 sums), so
+// the scores carry about 22 bits of q instead of 11. The power of two 2^e
+// keeps the largest |q'| of the row below 2^15 (e = 0 unless |q| >= 2^15, so
+// a q beyond the fp16 range never becomes inf) and is folded back into the
+// row's score scale.
+template <int D, bool ALIGNED, bool QSPLIT>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
@@ -297,9 +308,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     const int kv_len = p.kv_len(b);
     const int qo = p.q_off(b);
     const int ko = p.k_off(b);
+    const int qlen = p.q_len(b);
     int kv_lim = kv_len;
     if (p.causal) {
-      int64_t lim = (int64_t)qo + (p.M - 1) - ko + 1;
+      int64_t lim = (int64_t)qo + (qlen - 1) - ko + 1;
       if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
     }
     const int t_end = min(kv_lim, g_stop << 4);
@@ -336,24 +348,51 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       }
 
       half8 qreg[KSTEPS];
+      half8 qlo[QSPLIT ? KSTEPS : 1];
+      float crow = c;  // score scale of this lane's row (log2 units)
+      const int64_t qrow_off = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 8 * quarter;
+      if constexpr (QSPLIT) {
+        const float* qf = reinterpret_cast<const float*>(p.q);
+        floatx4 x[KSTEPS][2];
+        float amax = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
-        if (row_ok) {
-          const int64_t qoff = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 32 * kk + 8 * quarter;
-          if (p.q_f32) {
-            const floatx4 lo = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.q) + qoff);
-            const floatx4 hi =
-                *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.q) + qoff + 4);
-            qreg[kk] = half8{(f16)lo[0], (f16)lo[1], (f16)lo[2], (f16)lo[3],
-                             (f16)hi[0], (f16)hi[1], (f16)hi[2], (f16)hi[3]};
-          } else {
-            qreg[kk] = *reinterpret_cast<const half8*>(qp + qoff);
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            x[kk][h] = row_ok ? *reinterpret_cast<const floatx4*>(qf + qrow_off + 32 * kk + 4 * h)
+                              : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(x[kk][h][j]));
           }
-        } else {
-          qreg[kk] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
+        // the row's four quarters hold its D values
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        int ex = 0;
+        if (amax >= 32768.f && amax <= 3.0e38f) {
+          (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+          ex -= 15;                 // amax * 2^-ex in [2^14, 2^15)
+        }
+        const float down = ldexpf(1.f, -ex);
+        crow = c * ldexpf(1.f, ex);
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float v = x[kk][j >> 2][j & 3] * down;
+            const f16 hv = (f16)v;
+            qreg[kk][j] = hv;
+            qlo[kk][j] = (f16)(v - (float)hv);  // v - hv is exact in fp32
+          }
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          qreg[kk] = row_ok ? *reinterpret_cast<const half8*>(qp + qrow_off + 32 * kk)
+                            : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        if (p.rope_cos != nullptr && row_ok) rope_fragment<KSTEPS, 32>(qreg, p, qo + qi, 8 * quarter);
       }
-      if (p.rope_cos != nullptr && row_ok) rope_fragment<KSTEPS, 32>(qreg, p, qo + qi, 8 * quarter);
 
       float m_ref = -INFINITY;  // scaled (log2) reference max of the row
       float l_run = 0.f;
@@ -372,11 +411,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qreg[kk],
                                                      s, 0, 0, 0);
         }
+        if constexpr (QSPLIT) {
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk) {
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qlo[kk],
+                                                       s, 0, 0, 0);
+          }
+        }
         // lane holds tokens t0 + 4*quarter + i of row n
         float sv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim ? s[i] : -INFINITY;
-        const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
+        const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * crow;
         if (__builtin_amdgcn_ballot_w64(gmax > m_ref + 8.f) != 0) {
           const float m_new = fmaxf(m_ref, gmax);
           const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
@@ -388,7 +434,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
         half4 pb;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, -m_use));
+        for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], crow, -m_use));
         l_run = __builtin_amdgcn_fdot2(half2v{pb[0], pb[1]}, ones, l_run, false);
         l_run = __builtin_amdgcn_fdot2(half2v{pb[2], pb[3]}, ones, l_run, false);
 #pragma unroll
@@ -546,7 +592,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   const int hk = p.kv_head(hq);
   float result[DPW];
   const int kv_len = p.kv_len(b);
-  if (hk < 0) {
+  if (qi >= p.q_len(b)) {
+    // padding row (q_lens): zeros
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) result[k] = 0.f;
+  } else if (hk < 0) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = __builtin_nanf("");
   } else if (kv_len == 0) {
@@ -658,33 +708,42 @@ int env_int(const char* name, int fallback) {
   return v > 0 ? v : fallback;
 }
 
-}  // namespace
+// The decode kernel variant a call runs: row loads from whole 16-token
+// groups (ALIGNED: pages of a multiple of 16 tokens, or contiguous rows D
+// apart), and the fp32-query split (the token-major entry, which always takes
+// the per-row loads).
+struct DecodeVariant {
+  bool aligned;
+  bool qsplit;
+};
 
-bool use_decode_path(int B, int M, int Hq, int Hk) {
-  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch) return false;
-  const int group = (Hq + Hk - 1) / Hk;
-  return M >= 1 && (int64_t)M * group <= 4 * kRows;
+DecodeVariant decode_variant(const AttnParams& p) {
+  DecodeVariant v;
+  v.qsplit = p.q_f32 != 0;
+  v.aligned = !v.qsplit && (p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D);
+  return v;
 }
 
-int resident_decode_wgs(int D, bool aligned) {
+template <int D>
+const void* decode_fn(DecodeVariant v) {
+  if (v.qsplit) return reinterpret_cast<const void*>(&decode_kernel<D, false, true>);
+  return v.aligned ? reinterpret_cast<const void*>(&decode_kernel<D, true, false>)
+                   : reinterpret_cast<const void*>(&decode_kernel<D, false, false>);
+}
+
+int resident_decode_wgs(int D, DecodeVariant var) {
   // Workgroups of the decode kernel that are resident at once on the current
   // device (CUs x workgroups per CU), cached per device and kernel variant.
   // Launching exactly this many gives every workgroup its equal share in a
   // single round; a partial second round leaves CUs idle.
-  static std::atomic<int> cache[64][4];
+  static std::atomic<int> cache[64][8];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  const int idx = (D == 128 ? 2 : 0) + (aligned ? 1 : 0);
+  const int idx = (D == 128 ? 4 : 0) + (var.qsplit ? 2 : 0) + (var.aligned ? 1 : 0);
   int v = cache[dev][idx].load(std::memory_order_relaxed);
   if (v > 0) return v;
   int cus = 0, per_cu = 0;
-  const void* fn = nullptr;
-  if (D == 128)
-    fn = aligned ? reinterpret_cast<const void*>(&decode_kernel<128, true>)
-                 : reinterpret_cast<const void*>(&decode_kernel<128, false>);
-  else
-    fn = aligned ? reinterpret_cast<const void*>(&decode_kernel<64, true>)
-                 : reinterpret_cast<const void*>(&decode_kernel<64, false>);
+  const void* fn = D == 128 ? decode_fn<128>(var) : decode_fn<64>(var);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDecodeThreads, 0) != hipSuccess) {
     (void)hipGetLastError();
@@ -695,9 +754,17 @@ int resident_decode_wgs(int D, bool aligned) {
   return v;
 }
 
-int decode_launch_wgs(const DecodePlan& plan, int D, bool aligned) {
+}  // namespace
+
+bool use_decode_path(int B, int M, int Hq, int Hk) {
+  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch) return false;
+  const int group = (Hq + Hk - 1) / Hk;
+  return M >= 1 && (int64_t)M * group <= 4 * kRows;
+}
+
+int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
   if (getenv("FA_DECODE_WGS") != nullptr) return plan.wgs;
-  const int r = resident_decode_wgs(D, aligned);
+  const int r = resident_decode_wgs(D, decode_variant(p));
   return r > 0 ? std::min(plan.wgs, r) : plan.wgs;
 }
 
@@ -733,25 +800,16 @@ void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
   const dim3 grid((unsigned)p.dec_wgs);
   const int rows = p.B * p.Hq * p.M;
-  const bool aligned = p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D;
+  const DecodeVariant var = decode_variant(p);
   const dim3 block(kDecodeThreads);
-  if (D == 128) {
-    if (aligned)
-      hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+  const void* fn = D == 128 ? decode_fn<128>(var) : decode_fn<64>(var);
+  void* args[] = {const_cast<AttnParams*>(&p)};
+  hipError_t e = hipLaunchKernel(fn, grid, block, args, 0, stream);
+  if (e != hipSuccess) return e;
+  if (D == 128)
     launch_combine<128>(p, rows, stream);
-  } else {
-    if (aligned)
-      hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+  else
     launch_combine<64>(p, rows, stream);
-  }
   return hipGetLastError();
 }
 

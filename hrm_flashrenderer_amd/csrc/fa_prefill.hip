@@ -180,8 +180,9 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   const int hk = p.kv_head(hq);
   if (hk < 0) {
     if (qrow < p.M) {
+      const f16 fill = qrow < p.q_len(b) ? (f16)__builtin_nanf("") : (f16)0.f;
       for (int d = half_id * (D / 2); d < (half_id + 1) * (D / 2); ++d)
-        op[(int64_t)qrow * D + d] = (f16)__builtin_nanf("");
+        op[(int64_t)qrow * D + d] = fill;
     }
     return;
   }
@@ -189,13 +190,14 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   const int kv_len = p.kv_len(b);
   const int qo = p.q_off(b);
   const int ko = p.k_off(b);
-  const int last_row = min(q0 + kBM, p.M) - 1;
-  const int wg_lim = row_key_limit(kv_len, p.causal, qo, ko, last_row);
+  const int qlen = p.q_len(b);  // rows at or past qlen are padding: zeros, no tiles
+  const int last_row = min(q0 + kBM, qlen) - 1;
+  const int wg_lim = q0 < qlen ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
   const int ntiles = (wg_lim + kBN - 1) / kBN;
 
   const int wrow0 = q0 + wave * 32;
-  const int wrow1 = min(wrow0 + 31, p.M - 1);
-  const bool wave_rows = wrow0 < p.M;
+  const int wrow1 = min(wrow0 + 31, qlen - 1);
+  const bool wave_rows = wrow0 < qlen;
   const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
   const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
   const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
@@ -297,15 +299,18 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
   if (qrow >= p.M) return;
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   // kv_len == 0: zeros (empty softmax times empty V); otherwise a row without
-  // visible keys gives 0 * inf = NaN, as the reference does.
+  // visible keys gives 0 * inf = NaN, as the reference does. Padding rows
+  // (qrow >= qlen) are zeros whatever their Q held.
+  const bool live = qrow < qlen;
   const float inv = kv_len == 0 ? 0.f : 1.f / l_tot;
   f16* orow = op + (int64_t)qrow * D;
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
-                            (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
+                      (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      if (!live) h = half4{0, 0, 0, 0};
       *reinterpret_cast<half4*>(orow + 32 * i + 8 * g + 4 * half_id) = h;
     }
   }
@@ -364,7 +369,7 @@ __device__ __forceinline__ float max16(const floatx16& s) {
 // word of Q) and its default replaces the value. Uniform (b, hq) give scalar
 // loads; per-lane ones give vector loads that all leave before one wait.
 struct SeqData {
-  int kv_len, hk, qo, ko;
+  int kv_len, hk, qo, ko, qlen;
 };
 
 __device__ __forceinline__ int ld_or(const int32_t* ptr, int idx, int dflt, const void* any) {
@@ -382,6 +387,8 @@ __device__ __forceinline__ SeqData seq_data(const AttnParams& p, int b, int hq) 
   d.hk = (hk >= 0 && hk < p.Hk) ? hk : -1;
   d.qo = ld_or(p.q_offsets, b, p.q_offset, p.q);
   d.ko = ld_or(p.k_offsets, b, p.k_offset, p.q);
+  const int ql = ld_or(p.q_lens, b, p.M, p.q);
+  d.qlen = ql < 0 ? 0 : ql > p.M ? p.M : ql;
   return d;
 }
 
@@ -602,7 +609,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // With `pre`, the sequence data of the chosen pair come from the loads that
   // ordered the pairs (kv_len_pre, hk_pre, qo_pre, ko_pre).
   bool pre = false;
-  int kv_len_pre = 0, hk_pre = 0, qo_pre = 0, ko_pre = 0;
+  int kv_len_pre = 0, hk_pre = 0, qo_pre = 0, ko_pre = 0, qlen_pre = 0;
   if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
     // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
     // x + 8, x + 16, ..., so sequences of different lengths spread over all
@@ -636,6 +643,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       hk_pre = __builtin_amdgcn_readlane(c.hk, j);
       qo_pre = __builtin_amdgcn_readlane(c.qo, j);
       ko_pre = __builtin_amdgcn_readlane(c.ko, j);
+      qlen_pre = __builtin_amdgcn_readlane(c.qlen, j);
       pre = true;
     }
     pair = x + 8 * j;
@@ -675,18 +683,19 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const int kv_len = pre ? kv_len_pre : sd.kv_len;
   const int qo = pre ? qo_pre : sd.qo;
   const int ko = pre ? ko_pre : sd.ko;
+  const int qlen = pre ? qlen_pre : sd.qlen;  // rows at or past qlen: padding (zeros, no tiles)
   const bool head_ok = hk >= 0;
   Table pages;
   pages.base = 0;
   pages.rows = Table::row_finish(p, b, req0);
   pages.hk_rows = head_ok ? (uint32_t)((int64_t)hk * (p.kv.stride_hk / D)) : 0u;
 
-  const int last_row = min(q0 + kBM, p.M) - 1;
-  const int wg_lim = head_ok ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
+  const int last_row = min(q0 + kBM, qlen) - 1;
+  const int wg_lim = head_ok && q0 < qlen ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
   const int ntiles = (wg_lim + BN - 1) / BN;
   const int wrow0 = q0 + wave * 32;
-  const int wrow1 = min(wrow0 + 31, p.M - 1);
-  const bool wave_rows = wrow0 < p.M;
+  const int wrow1 = min(wrow0 + 31, qlen - 1);
+  const bool wave_rows = wrow0 < qlen;
   const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
   const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
   const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
@@ -828,14 +837,16 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // half of 16-byte chunk 4i + g.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = !head_ok ? __builtin_nanf("") : kv_len == 0 ? 0.f : 1.f / l_tot;
+  const bool live = qrow < qlen;  // padding rows are zeros whatever their Q held
   __syncthreads();  // every wave has finished reading the last K/V stage
   const int lrow = wave * 32 + col;
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
-                            (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      half4 h = half4{(f16)(acc_o[i][4 * g + 0] * inv), (f16)(acc_o[i][4 * g + 1] * inv),
+                      (f16)(acc_o[i][4 * g + 2] * inv), (f16)(acc_o[i][4 * g + 3] * inv)};
+      if (!live) h = half4{0, 0, 0, 0};
       const int chunk = (4 * i + g) ^ C::swz_k(lrow);
       *reinterpret_cast<half4*>(smem + lrow * C::ROWB + 16 * chunk + 8 * half_id) = h;
     }

@@ -26,6 +26,19 @@ ids on the device:
 
 The operators consume the cache through `get()` / `block_table`, or directly
 through `attention()`.
+
+`layout="per_sequence"` keeps the reference's own layout instead: one page
+array per sequence, `k_pages` `[bsz, Hk, P, PS, D]`, with no block table (the
+kernels' identity page map). `get()` then feeds the reference's unchanged
+caller (engine/llama_tp.py:186-200), which passes no block table. All
+sequences grow together by doubling P with one copy, as the reference does
+with its power-of-two growth (llama_tp.py:47-57). Appends and lengths work
+the same way in both layouts.
+
+`append(..., positions=[B, T])` takes any positions per row, which is the
+reference's general path (llama_tp.py:80-99). Consecutive rows are one
+append launch. Other rows are one scatter launch (`paged_kv_scatter`) instead
+of the reference's per-row Python copies.
 """
 from __future__ import annotations
 
@@ -34,7 +47,7 @@ from typing import List, Optional, Sequence, Tuple, Union
 import numpy as np
 import torch
 
-from .ops import flash_attn_paged, paged_kv_append
+from .ops import flash_attn_paged, paged_kv_append, paged_kv_scatter
 
 PositionsLike = Union[None, int, torch.Tensor]
 
@@ -45,13 +58,15 @@ class PagedKVCache:
     Arguments follow the reference constructor (engine/llama_tp.py:24-33):
     `init_pages` is the initial number of pages per sequence, so the pool
     starts with `bsz * init_pages` pages. `max_seq_len` (optional) sizes the
-    block table up front; it widens on demand otherwise.
+    block table (or, per sequence, the pages) up front; it grows on demand
+    otherwise. `layout` is "pool" (one shared pool with a block table) or
+    "per_sequence" (the reference's `[bsz, Hk, P, PS, D]`, no block table).
     """
 
     def __init__(self, bsz: int, kv_heads: int, head_dim: int, page_size: int = 128,
                  init_pages: int = 4, device: Union[str, torch.device] = "cuda",
                  dtype: torch.dtype = torch.float16, *, max_seq_len: Optional[int] = None,
-                 pool_pages: Optional[int] = None):
+                 pool_pages: Optional[int] = None, layout: str = "pool"):
         self.bsz = int(bsz)
         self.kv_heads = int(kv_heads)
         self.head_dim = int(head_dim)
@@ -60,6 +75,24 @@ class PagedKVCache:
         self.dtype = dtype
         if self.bsz <= 0 or self.kv_heads <= 0 or self.head_dim <= 0 or self.page_size <= 0:
             raise ValueError("bsz, kv_heads, head_dim and page_size must be positive")
+        if layout not in ("pool", "per_sequence"):
+            raise ValueError('layout must be "pool" or "per_sequence"')
+        self.layout = layout
+        self._pages_of = [0] * self.bsz       # mapped logical pages per sequence
+        self.lengths = [0] * self.bsz         # host copy of seqlen
+        self.seqlen = torch.zeros(self.bsz, dtype=torch.int32, device=self.device)
+        self.cur_len = 0                      # max length, as the reference tracks it
+        if layout == "per_sequence":
+            per_seq = max(1, int(init_pages))
+            if max_seq_len is not None:
+                per_seq = max(per_seq, -(-int(max_seq_len) // self.page_size))
+            self.k_pages = torch.empty(self.bsz, self.kv_heads, per_seq, self.page_size,
+                                       self.head_dim, device=self.device, dtype=dtype)
+            self.v_pages = torch.empty_like(self.k_pages)
+            self._bt_host = None
+            self._block_table = None
+            self._free: List[int] = []
+            return
         npages = int(pool_pages) if pool_pages is not None else self.bsz * max(1, int(init_pages))
         npages = max(1, npages)
         self.k_pages = torch.empty(1, self.kv_heads, npages, self.page_size, self.head_dim,
@@ -72,22 +105,23 @@ class PagedKVCache:
         self._block_table = torch.full((self.bsz, blocks), -1, dtype=torch.int32,
                                        device=self.device)
         self._free: List[int] = list(range(npages - 1, -1, -1))  # pop() yields low ids first
-        self._pages_of = [0] * self.bsz       # mapped logical pages per sequence
-        self.lengths = [0] * self.bsz         # host copy of seqlen
-        self.seqlen = torch.zeros(self.bsz, dtype=torch.int32, device=self.device)
-        self.cur_len = 0                      # max length, as the reference tracks it
 
     # ------------------------------------------------------------ queries --
     @property
     def pool_pages(self) -> int:
-        return int(self.k_pages.size(2))
+        """Physical (page, all KV heads) slots held on the device."""
+        return int(self.k_pages.size(0) * self.k_pages.size(2))
 
     @property
     def max_blocks(self) -> int:
+        """Logical pages a sequence can hold without growing the cache."""
+        if self._bt_host is None:
+            return int(self.k_pages.size(2))
         return int(self._bt_host.shape[1])
 
     @property
-    def block_table(self) -> torch.Tensor:
+    def block_table(self) -> Optional[torch.Tensor]:
+        """int32 [bsz, max_blocks] page map of the pool layout (None per sequence)."""
         return self._block_table
 
     @property
@@ -95,8 +129,11 @@ class PagedKVCache:
         return len(self._free)
 
     def get(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """(k_pages, v_pages, seqlen) as in the reference (llama_tp.py:101-102);
-        the operators also need `block_table=cache.block_table`."""
+        """(k_pages, v_pages, seqlen) as in the reference (llama_tp.py:101-102).
+        With the pool layout the operators also need
+        `block_table=cache.block_table`; without it they raise "B mismatch"
+        with that hint. With layout="per_sequence" the reference's call
+        (llama_tp.py:187-200, no block table) works as it stands."""
         return self.k_pages, self.v_pages, self.seqlen
 
     # --------------------------------------------------------- allocation --
@@ -109,6 +146,13 @@ class PagedKVCache:
         self._reserve_many([(b, need)])
 
     def _reserve_many(self, wants: Sequence[Tuple[int, int]]) -> None:
+        if self._bt_host is None:
+            need = max((n for _, n in wants), default=0)
+            if need > self.k_pages.size(2):
+                self._grow_per_sequence(max(need, 2 * int(self.k_pages.size(2))))
+            for b, n in wants:
+                self._pages_of[b] = max(self._pages_of[b], n)
+            return
         new_entries = []
         for b, need in wants:
             have = self._pages_of[b]
@@ -140,6 +184,15 @@ class PagedKVCache:
         dev[:, :old.shape[1]] = self._block_table
         self._block_table = dev
 
+    def _grow_per_sequence(self, pages: int) -> None:
+        old = int(self.k_pages.size(2))
+        k = torch.empty(self.bsz, self.kv_heads, pages, self.page_size, self.head_dim,
+                        device=self.device, dtype=self.dtype)
+        v = torch.empty_like(k)
+        k[:, :, :old] = self.k_pages
+        v[:, :, :old] = self.v_pages
+        self.k_pages, self.v_pages = k, v
+
     def _grow_pool(self, at_least: int) -> None:
         old = self.pool_pages
         new = max(2 * old, old + int(at_least))
@@ -155,7 +208,9 @@ class PagedKVCache:
     def free(self, b: int) -> None:
         """Release sequence b's pages and set its length to zero."""
         n = self._pages_of[b]
-        if n:
+        if n and self._bt_host is None:
+            self._pages_of[b] = 0   # per-sequence pages stay allocated
+        elif n:
             ids = self._bt_host[b, :n].tolist()
             self._free.extend(reversed(ids))
             self._bt_host[b, :n] = -1
@@ -170,7 +225,9 @@ class PagedKVCache:
         self.cur_len = 0
 
     # ------------------------------------------------------------- append --
-    def _starts(self, positions: PositionsLike, T: int) -> List[int]:
+    def _starts(self, positions: PositionsLike, T: int) -> Union[List[int], torch.Tensor]:
+        """Per-sequence start positions of consecutive rows, or the host
+        int64 [B, T] positions when some row is not consecutive."""
         if positions is None:
             return list(self.lengths)
         if isinstance(positions, int):
@@ -193,7 +250,7 @@ class PagedKVCache:
             starts = pos[:, 0].tolist() if T else [0] * self.bsz
             want = torch.tensor(starts, dtype=torch.int64)[:, None] + torch.arange(T)[None]
             if T and not torch.equal(pos.to(torch.int64), want):
-                raise ValueError("each row of positions [B, T] must be consecutive")
+                return pos.to(torch.int64)   # scattered rows
             return [int(s) for s in starts]
         raise ValueError("positions must be None, an int, [T] or [B, T]")
 
@@ -204,10 +261,14 @@ class PagedKVCache:
 
         `positions`: None (append at each sequence's current length), an int
         or a `[T]` tensor (same start for all sequences, as the reference's
-        fast path, llama_tp.py:65-78), or `[B, T]` (per-sequence starts; each
-        row consecutive). One kernel launch in every case. `rope=(cos, sin)`
-        rotates the keys at their positions in the same launch (the
-        reference's apply_rope on K, engine/llama_tp.py:183).
+        fast path, llama_tp.py:65-78), or `[B, T]` (any positions per row,
+        the reference's general path, llama_tp.py:80-99: a row of
+        consecutive positions is appended from its start, other rows are
+        scattered token by token; of two tokens of one row at the same
+        position the later one is kept, as in the reference's loop). One
+        kernel launch in every case. `rope=(cos, sin)` rotates each key at
+        its own position in the same launch (the reference's apply_rope on
+        K, engine/llama_tp.py:183).
 
         `valid` (host ints, one per sequence, each <= T): only the first
         valid[b] tokens of sequence b are real (a ragged chunk padded to T);
@@ -222,6 +283,11 @@ class PagedKVCache:
         if B != self.bsz or Hk != self.kv_heads or D != self.head_dim:
             raise ValueError("k_new must be [bsz, kv_heads, T, head_dim]")
         starts = self._starts(positions, T)
+        if isinstance(starts, torch.Tensor):
+            if valid is not None:
+                raise ValueError("valid applies to rows of consecutive positions only")
+            self._scatter(k_new, v_new, starts, rope)
+            return
         if any(s < 0 for s in starts):
             raise ValueError("positions must be non-negative")
         if valid is not None:
@@ -262,6 +328,22 @@ class PagedKVCache:
                 self.lengths[b] = max(self.lengths[b], st + n)
         self.cur_len = max(self.lengths)
 
+    def _scatter(self, k_new: torch.Tensor, v_new: torch.Tensor, pos: torch.Tensor, rope) -> None:
+        """Token t of sequence b at pos[b, t] (host int64 [B, T]), one launch."""
+        if bool((pos < 0).any()):
+            raise ValueError("positions must be non-negative")
+        ends = (pos.max(dim=1).values + 1).tolist()
+        self._reserve_many([(b, -(-int(e) // self.page_size)) for b, e in enumerate(ends)])
+        keep = keep_last_of_duplicates(pos.numpy())
+        pos_dev = torch.from_numpy(keep.astype(np.int32)).to(self.device, non_blocking=True)
+        paged_kv_scatter(self.k_pages, self.v_pages, k_new.contiguous(), v_new.contiguous(),
+                         pos_dev, self.page_size, block_table=self._block_table, rope=rope)
+        ends_dev = torch.tensor(ends, dtype=torch.int32).to(self.device, non_blocking=True)
+        torch.maximum(self.seqlen, ends_dev, out=self.seqlen)
+        for b, e in enumerate(ends):
+            self.lengths[b] = max(self.lengths[b], int(e))
+        self.cur_len = max(self.lengths)
+
     def _set_lengths(self, new: dict, shrink: bool = False) -> None:
         for b, n in new.items():
             if shrink or n > self.lengths[b]:
@@ -271,12 +353,89 @@ class PagedKVCache:
 
     # ---------------------------------------------------------- attention --
     def attention(self, q: torch.Tensor, head_map: torch.Tensor, causal: bool,
-                  q_offset: Union[int, torch.Tensor] = 0, *, rope=None) -> torch.Tensor:
+                  q_offset: Union[int, torch.Tensor] = 0, *, rope=None,
+                  q_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
         """flash_attn_paged over this cache (block table included); `rope`
-        rotates q in the kernel at positions q_offset + i."""
+        rotates q in the kernel at positions q_offset + i; `q_lens` (int32
+        [B] on the device) marks rows i >= q_lens[b] as padding (zeros)."""
         return flash_attn_paged(q, self.k_pages, self.v_pages, self.seqlen, self.page_size,
                                 head_map, causal, q_offset, 0, block_table=self._block_table,
-                                rope=rope)
+                                rope=rope, q_lens=q_lens)
+
+    def prefill_chunk(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                      starts: Sequence[int], valid: Sequence[int], head_map: torch.Tensor,
+                      *, rope=None) -> torch.Tensor:
+        """One chunk of a chunked prefill in which every sequence has its own
+        position (a `chunked_prefill_schedule` entry).
+
+        Row i < valid[b] of sequence b is the prompt token at position
+        starts[b] + i; rows past valid[b] are padding. The chunk's K/V are
+        appended at those positions (padding maps no page and never covers a
+        live token), then the chunk attends causally over each sequence's
+        cache with q_offset = starts (int32 [B]) and q_lens = valid, so the
+        kernels skip the padding rows' tiles and return zeros for them.
+        Returns the attention output [B, Hq, T, D]. This generalises the
+        reference's generate loop (engine/llama_tp.py:338-354), which runs
+        equal-length prompts at one shared position.
+        """
+        B, _, T, _ = k_new.shape
+        starts = [int(x) for x in starts]
+        valid = [int(x) for x in valid]
+        if len(starts) != B or len(valid) != B:
+            raise ValueError("starts and valid must hold B entries")
+        pos = torch.tensor(starts, dtype=torch.int64)[:, None] + torch.arange(T)[None]
+        self.append(k_new, v_new, pos, valid=valid, rope=rope)
+        qo = torch.tensor(starts, dtype=torch.int32).to(self.device, non_blocking=True)
+        ql = torch.tensor(valid, dtype=torch.int32).to(self.device, non_blocking=True)
+        return self.attention(q, head_map, True, qo, rope=rope, q_lens=ql)
+
+
+def chunked_prefill_schedule(prompt_lengths: Sequence[int], chunk_tokens: int,
+                             cached_lengths: Optional[Sequence[int]] = None
+                             ) -> List[Tuple[List[int], List[int]]]:
+    """Chunks of a chunked prefill in which each sequence advances from its
+    own position.
+
+    Sequence b already holds cached_lengths[b] tokens (0 by default; a shared
+    prefix or an earlier turn) and has prompt_lengths[b] new tokens. Chunk c
+    takes new tokens [c * chunk_tokens, (c + 1) * chunk_tokens) of every
+    sequence, at positions cached_lengths[b] + c * chunk_tokens + i. Returns
+    [(starts, valid), ...]: starts[b] is the chunk's first position in
+    sequence b (its q_offset), valid[b] how many of its rows are real (its
+    q_lens; 0 once the sequence's prompt is done). A chunk's row count is
+    max(valid). Feed each entry to `PagedKVCache.prefill_chunk`. With equal
+    prompts and no cache this is the reference's loop (engine/llama_tp.py:
+    338-354); ragged prompts and prefixes need no padding work, because the
+    kernels skip rows past valid[b].
+    """
+    if chunk_tokens <= 0:
+        raise ValueError("chunk_tokens must be positive")
+    n = [int(x) for x in prompt_lengths]
+    cached = [0] * len(n) if cached_lengths is None else [int(x) for x in cached_lengths]
+    if len(cached) != len(n):
+        raise ValueError("cached_lengths must match prompt_lengths")
+    if any(x < 0 for x in n) or any(x < 0 for x in cached):
+        raise ValueError("lengths must be non-negative")
+    plan = []
+    for c in range(0, max(n, default=0), chunk_tokens):
+        valid = [max(0, min(chunk_tokens, x - c)) for x in n]
+        plan.append(([cb + c for cb in cached], valid))
+    return plan
+
+
+def keep_last_of_duplicates(pos: np.ndarray) -> np.ndarray:
+    """Copy of `pos` [B, T] in which every position that occurs again later
+    in its row is replaced by -1 (a slot the scatter kernel skips), so the
+    last token written to a position wins, as in the reference's loop over t
+    (engine/llama_tp.py:92-97)."""
+    keep = np.array(pos, dtype=np.int64, copy=True)
+    T = keep.shape[1] if keep.ndim == 2 else 0
+    for row in keep:
+        _, last_rev = np.unique(row[::-1], return_index=True)
+        drop = np.ones(T, dtype=bool)
+        drop[T - 1 - last_rev] = False
+        row[drop] = -1
+    return keep
 
 
 def chunked_prefill_plan(prompt_lengths: Sequence[int], chunk_tokens: int) -> List[Tuple[int, List[int]]]:

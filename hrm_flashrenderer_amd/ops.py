@@ -158,7 +158,8 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
                          causal: bool, q_offset: int, k_offset: int,
                          q_offsets: Optional[torch.Tensor], k_offsets: Optional[torch.Tensor],
                          block_table: Optional[torch.Tensor], rope_cos: Optional[torch.Tensor],
-                         rope_sin: Optional[torch.Tensor]) -> torch.Tensor:
+                         rope_sin: Optional[torch.Tensor],
+                         q_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
     lib = _lib.load()
     o = torch.empty_like(q)
     B, Hq, M, D = q.shape
@@ -171,7 +172,7 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
         args = (q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(),
                 page_size, head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P,
                 int(causal), q_offset, k_offset, _ptr(q_offsets), _ptr(k_offsets),
-                _ptr(block_table), max_blocks, _ptr(ws), ws_bytes)
+                _ptr(q_lens), _ptr(block_table), max_blocks, _ptr(ws), ws_bytes)
         if rope_cos is None:
             _lib.check(lib.fa_flash_attn_paged_fwd(*args, stream))
         else:
@@ -182,7 +183,7 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
 
 @_flash_attn_paged_op.register_fake
 def _(q, k_pages, v_pages, seqlen, page_size, head_map, causal, q_offset, k_offset, q_offsets,
-      k_offsets, block_table, rope_cos, rope_sin):
+      k_offsets, block_table, rope_cos, rope_sin, q_lens=None):
     return torch.empty_like(q)
 
 
@@ -212,9 +213,45 @@ def _(k_pages, v_pages, k_new, v_new, start_pos, start_positions, page_size, blo
     return None
 
 
+@torch.library.custom_op("hrm_fa::paged_kv_scatter", mutates_args=("k_pages", "v_pages"))
+def _paged_kv_scatter_op(k_pages: torch.Tensor, v_pages: torch.Tensor, k_new: torch.Tensor,
+                         v_new: torch.Tensor, positions: torch.Tensor, page_size: int,
+                         block_table: Optional[torch.Tensor], rope_cos: Optional[torch.Tensor],
+                         rope_sin: Optional[torch.Tensor]) -> None:
+    lib = _lib.load()
+    B, Hk, T, D = k_new.shape
+    NB, P = k_pages.size(0), k_pages.size(2)
+    max_blocks = int(block_table.size(1)) if block_table is not None else 0
+    with _DeviceScope(k_pages) as stream:
+        _lib.check(lib.fa_paged_kv_scatter(
+            k_pages.data_ptr(), v_pages.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+            B, Hk, T, D, NB, P, page_size, positions.data_ptr(), _ptr(block_table), max_blocks,
+            _ptr(rope_cos), _ptr(rope_sin), rope_cos.size(0) if rope_cos is not None else 0,
+            stream))
+
+
+@_paged_kv_scatter_op.register_fake
+def _(k_pages, v_pages, k_new, v_new, positions, page_size, block_table, rope_cos, rope_sin):
+    return None
+
+
 # --------------------------------------------------------------------------
 # public API
 # --------------------------------------------------------------------------
+
+_SHARED_POOL_HINT = ("k_pages holds one shared page pool (size(0) == 1) for {B} sequences: "
+                     "pass block_table= (PagedKVCache.block_table) to map each sequence's "
+                     "pages into it")
+
+
+def _check_batch(q_batch: int, pool_rows: int, block_table) -> None:
+    """'B mismatch' as the reference raises it (csrc/ext.cpp:58), with a hint
+    when the pages are a shared pool that needs its block table."""
+    if block_table is not None or q_batch == pool_rows:
+        return
+    if pool_rows == 1 and q_batch > 1:
+        raise RuntimeError("B mismatch: " + _SHARED_POOL_HINT.format(B=q_batch))
+    raise RuntimeError("B mismatch")
 
 def validate_flash_attn(q, k, v, require_device: bool = True) -> None:
     """Argument checks of flash_attn, in the order of csrc/ext.cpp:31-38."""
@@ -263,7 +300,7 @@ def validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
     _check(k_pages.dim() == 5 and v_pages.dim() == 5, "k_pages/v_pages [B,Hk,P,PS,D]")
     _check(k_pages.shape == v_pages.shape, "k_pages/v_pages mismatch")
     B = q.size(0)
-    _check(block_table is not None or q.size(0) == k_pages.size(0), "B mismatch")
+    _check_batch(B, k_pages.size(0), block_table)
     _check(head_map.dim() == 1 and q.size(1) == head_map.size(0), "Hq mismatch")
     _check(k_pages.size(3) == page_size, "page_size mismatch")
     _check(k_pages.size(4) == q.size(3), "D mismatch")
@@ -276,7 +313,8 @@ def validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
 
 
 def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
-                     causal=True, q_offset=0, k_offset=0, *, block_table=None, rope=None):
+                     causal=True, q_offset=0, k_offset=0, *, block_table=None, rope=None,
+                     q_lens=None):
     """Attention of q over paged K/V (prefill chunk or decode).
 
     Reference: flashattention_custom/ops.py:85-92 -> csrc/ext.cpp:42-68.
@@ -284,6 +322,9 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
     head_map int32 [Hq]. Returns a new tensor shaped like q. With
     rope=(cos, sin), q is rotated in the kernel (engine/rope.py:15-24) at
     positions q_offset + i; a scalar q_offset must keep them inside the table.
+    With q_lens (int32 device tensor [B]), only rows i < q_lens[b] of
+    sequence b are live (a ragged chunk padded to M rows): the others are not
+    computed and come out as zeros.
     """
     page_size = int(page_size)
     validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
@@ -295,12 +336,19 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
         _check(qo >= 0 and qo + q.size(2) <= cos.size(0),
                f"positions {qo}..{qo + q.size(2) - 1} are outside the rotary table "
                f"of {cos.size(0)}")
+    if q_lens is not None:
+        _check(isinstance(q_lens, torch.Tensor), "q_lens [B] required")
+        _check(q_lens.is_cuda and q_lens.device == q.device, "q_lens tensor must be CUDA")
+        _check(q_lens.dtype == torch.int32, "q_lens int32 required")
+        _check(q_lens.is_contiguous(), "contiguous required")
+        _check(q_lens.dim() == 1 and q_lens.numel() == B, "q_lens [B] required")
     return _flash_attn_paged_op(q, k_pages, v_pages, seqlen, page_size, head_map, bool(causal),
-                                qo, ko, qo_t, ko_t, block_table, cos, sin)
+                                qo, ko, qo_t, ko_t, block_table, cos, sin, q_lens)
 
 
 def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,
-                             block_table=None, require_device: bool = True):
+                             block_table=None, require_device: bool = True,
+                             check_range: bool = True):
     """Argument checks of paged_kv_append (csrc/ext.cpp:78-87 order, then the
     extensions); returns (scalar start, per-sequence start tensor or None)."""
     if require_device:
@@ -314,7 +362,7 @@ def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_siz
     _check(k_pages.shape == v_pages.shape, "k_pages/v_pages mismatch")
     _check(k_new.shape == v_new.shape, "k_new/v_new mismatch")
     B, Hk, T, D = k_new.shape
-    _check(block_table is not None or k_pages.size(0) == B, "B mismatch")
+    _check_batch(B, k_pages.size(0), block_table)
     _check(k_pages.size(1) == Hk, "Hk mismatch")
     _check(k_pages.size(3) == page_size, "page_size mismatch")
     _check(k_pages.size(4) == D, "D mismatch")
@@ -324,7 +372,7 @@ def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_siz
            "tensors must be on one device")
     max_blocks = _check_block_table(block_table, B, dev, require_device)
     sp, sp_t = _per_seq(start_pos, B, "start_pos", dev, require_device)
-    if sp_t is None and T > 0:
+    if check_range and sp_t is None and T > 0:
         cap = (max_blocks if block_table is not None else k_pages.size(2)) * page_size
         _check(sp >= 0 and sp + T <= cap,
                f"start_pos {sp} + T {T} exceeds the page capacity {cap}")
@@ -353,3 +401,33 @@ def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, blo
                    f"positions {sp}..{sp + k_new.size(2) - 1} are outside the rotary table "
                    f"of {cos.size(0)}")
     _paged_kv_append_op(k_pages, v_pages, k_new, v_new, sp, sp_t, page_size, block_table, cos, sin)
+
+
+def paged_kv_scatter(k_pages, v_pages, k_new, v_new, positions, page_size, *, block_table=None,
+                     rope=None):
+    """Write token t of sequence b at positions[b, t], in place: the general
+    [B, T] path of the reference's cache (engine/llama_tp.py:80-99) as one
+    kernel launch instead of a Python loop of row copies.
+
+    positions: int32 device tensor [B, T]. Negative positions, and positions
+    whose page is beyond the capacity or unmapped, are skipped. Positions of
+    one sequence should be distinct: the reference's loop keeps the last of
+    duplicates, and here their order is unspecified (PagedKVCache.append
+    removes earlier duplicates before it calls this). rope=(cos, sin) rotates
+    each key at its own position. The caller updates seqlen, as the reference
+    does (engine/llama_tp.py:88-91).
+    """
+    page_size = int(page_size)
+    validate_paged_kv_append(k_pages, v_pages, k_new, v_new, 0, page_size, block_table,
+                             check_range=False)
+    B, T = k_new.size(0), k_new.size(2)
+    _check(isinstance(positions, torch.Tensor), "positions [B, T] required")
+    _check(positions.is_cuda and positions.device == k_pages.device, "positions must be CUDA")
+    _check(positions.dtype == torch.int32, "positions int32 required")
+    _check(positions.is_contiguous(), "contiguous required")
+    _check(positions.dim() == 2 and tuple(positions.shape) == (B, T), "positions [B, T] required")
+    cos, sin = _check_rope(rope, k_new.size(3), k_new.device)
+    if cos is not None:
+        _check(k_new.size(3) % 16 == 0, "rotary append needs head_dim a multiple of 16")
+    _paged_kv_scatter_op(k_pages, v_pages, k_new, v_new, positions, page_size, block_table,
+                         cos, sin)

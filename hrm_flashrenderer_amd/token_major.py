@@ -8,8 +8,11 @@ h % KVH, and the output is fp32 [H, Dh].
 
 `decode_token_major` runs that step on this library's split-K decode kernels
 through the C entry point fa_decode_token_major (the engine's C++ host code
-calls the same entry point directly). Q is rounded to fp16 for the matrix
-cores; scores, softmax and the output accumulate in fp32.
+calls the same entry point directly). The engine computes q . k in fp32
+(:573-577); the kernel splits each query row into fp16 hi and lo parts (after
+a power-of-two prescale when |q| >= 2^15) and takes both through the matrix
+cores, so the scores keep about 22 bits of q. Softmax and the output
+accumulate in fp32.
 """
 from __future__ import annotations
 

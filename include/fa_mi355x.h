@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 /* element type of q / k / v / o */
 #define FA_DTYPE_F16 0
@@ -82,6 +82,12 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
  *   block_table : nullable int32 [B, max_blocks] (see header comment);
  *                 without it NB must equal B.
  *   Visibility and offsets as in fa_flash_attn_fwd with N = seqlen[b].
+ *   q_lens   : nullable int32 [B]: only query rows i < q_lens[b] of sequence
+ *              b are live (a ragged chunk padded to M rows); rows at or past
+ *              it are not computed and come out as zeros. NULL: all M rows.
+ *              An additive extension for chunked prefill with per-sequence
+ *              offsets (the reference's generate loop, engine/llama_tp.py:
+ *              338-354, runs equal-length chunks only).
  *   workspace : device scratch of at least fa_paged_workspace_bytes(...)
  *               bytes for the same arguments (may be NULL when that is 0);
  *               its contents need no initialisation.
@@ -92,6 +98,7 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
                             int B, int Hq, int M, int D, int NB, int Hk, int P,
                             int causal, int64_t q_offset, int64_t k_offset,
                             const int32_t* q_offsets, const int32_t* k_offsets,
+                            const int32_t* q_lens,
                             const int32_t* block_table, int max_blocks,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
@@ -137,6 +144,7 @@ int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void*
                                  int B, int Hq, int M, int D, int NB, int Hk, int P,
                                  int causal, int64_t q_offset, int64_t k_offset,
                                  const int32_t* q_offsets, const int32_t* k_offsets,
+                                 const int32_t* q_lens,
                                  const int32_t* block_table, int max_blocks,
                                  void* workspace, size_t workspace_bytes,
                                  const void* rope_cos, const void* rope_sin, int rope_len,
@@ -158,6 +166,29 @@ int fa_paged_kv_append_rope(void* k_pages, void* v_pages,
                             void* stream);
 
 /*
+ * Write token t of sequence b at its own position positions[b * T + t], in
+ * place (same K/V and page layouts as fa_paged_kv_append). Replaces the
+ * general [B, T] path of the reference's cache, PagedKVCache.append
+ * (engine/llama_tp.py:80-99), which scatters one (b, t) row at a time from
+ * Python. One kernel launch; nothing is read back.
+ *   positions : int32 [B, T] device buffer. A negative position, or one whose
+ *               page is beyond the capacity or unmapped, is skipped. Two
+ *               tokens of one sequence at the same position write the same
+ *               slot in an unspecified order (the caller keeps the last one,
+ *               as the reference's loop does, by passing -1 for the others).
+ *   rope_cos, rope_sin : nullable fp16 [rope_len, D/2] tables; when given,
+ *               each key row is rotated at its own position as in
+ *               fa_paged_kv_append_rope (D % 16 == 0).
+ * The caller updates seqlen (the reference sets seqlen[b] to at least
+ * max_t positions[b, t] + 1, engine/llama_tp.py:88-91).
+ */
+int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
+                        int B, int Hk, int T, int D, int NB, int P, int page_size,
+                        const int32_t* positions, const int32_t* block_table, int max_blocks,
+                        const void* rope_cos, const void* rope_sin, int rope_len,
+                        void* stream);
+
+/*
  * Single-sequence decode attention over a token-major fp16 KV cache: the
  * cache layout, head mapping and fp32 input/output of the reference's INT8
  * engine decode step (attn_decode, scripts/deepseek_native_engine.sh:562-604,
@@ -167,8 +198,14 @@ int fa_paged_kv_append_rope(void* k_pages, void* v_pages,
  *   q, out           : fp32 [H, Dh]
  *   k_cache, v_cache : fp16 [>= t + 1, KVH, Dh]; row j of KV head kvh at
  *                      element j*KVH*Dh + kvh*Dh (the engine's Kc/Vc, :553-559)
- * Q is rounded to fp16 for the matrix cores; scores, softmax and the output
- * accumulate in fp32. A head_map entry outside [0, KVH) yields NaN rows.
+ * Precision (the engine computes q . k in fp32, :573-577): each query row is
+ * scaled by 2^-e (e = 0 unless max|q| >= 2^15, so q beyond the fp16 range
+ * does not overflow) and split into fp16 parts q_hi + q_lo, both multiplied
+ * by K on the matrix cores with fp32 accumulation. The scores then carry q to
+ * about 2^-22 relative (against 2^-11 for q rounded to fp16, which at logits
+ * of 30-70 already exceeds the 2e-3 + 1e-2|ref| bar). Softmax and the output
+ * accumulate in fp32; the softmax weights enter the P.V product as fp16
+ * (2^-11 relative each). A head_map entry outside [0, KVH) yields NaN rows.
  * workspace: fa_decode_token_major_workspace_bytes(H, KVH, Dh, t_max) bytes
  * for any t <= t_max (0 when the shape is unsupported).
  */

@@ -33,7 +33,7 @@ def test_header_declares_expected_entry_points():
         "fa_abi_version", "fa_decode_token_major", "fa_decode_token_major_workspace_bytes",
         "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd",
         "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
-        "fa_paged_kv_append_rope", "fa_paged_workspace_bytes"])
+        "fa_paged_kv_append_rope", "fa_paged_kv_scatter", "fa_paged_workspace_bytes"])
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -62,22 +62,25 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     assert rc == -1 and msg == "fp16 or fp32 required"
     # paged: pool batch must equal B without a block table; page_size positive
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 3, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 3, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
+        None))
     assert rc == -1 and msg == "B mismatch"
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 0, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+        P, P, P, P, 0, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
+        None))
     assert rc == -1 and msg == "page_size mismatch"
     # decode path without its workspace
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0, None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
+        None))
     assert rc == -3 and msg.startswith("workspace of")
     rc, msg = _status_and_message(lib.fa_paged_kv_append(
         P, P, P, P, 2, 4, 3, 12, 2, 4, 16, 0, None, None, 0, None))
     assert rc == -1 and msg == "head_dim must be a multiple of 8"
     # rotary variants: tables required; the fused append needs D % 16 == 0
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_rope_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, 0, None, 0,
-        None, None, 0, None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None,
+        0, None, None, 0, None))
     assert rc == -1 and msg == "rotary tables cos/sin [L, D/2] required"
     rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
         P, P, P, P, 2, 4, 3, 128, 2, 4, 16, 0, None, None, 0, None, None, 0, None))
@@ -85,6 +88,18 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
         P, P, P, P, 2, 4, 3, 24, 2, 4, 16, 0, None, None, 0, P, P, 64, None))
     assert rc == -1 and msg == "rotary append needs head_dim a multiple of 16"
+    # per-token scatter: positions required when there is work; rope tables in pairs
+    sc = lib.fa_paged_kv_scatter
+    rc, msg = _status_and_message(sc(P, P, P, P, 2, 4, 3, 128, 2, 4, 16, None, None, 0,
+                                     None, None, 0, None))
+    assert rc == -1 and msg == "positions [B, T] required"
+    rc, msg = _status_and_message(sc(P, P, P, P, 2, 4, 3, 128, 2, 4, 16, P, None, 0,
+                                     P, None, 64, None))
+    assert rc == -1 and msg == "rotary tables cos/sin [L, D/2] required"
+    rc, msg = _status_and_message(sc(P, P, P, P, 2, 4, 3, 128, 3, 4, 16, P, None, 0,
+                                     None, None, 0, None))
+    assert rc == -1 and msg == "B mismatch"
+    assert sc(P, P, P, P, 2, 4, 0, 128, 2, 4, 16, None, None, 0, None, None, 0, None) == 0
     # token-major decode (the INT8 engine's cache): shapes, scale, workspace
     tm = lib.fa_decode_token_major
     rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 96, 0.1, None, P, 1 << 20, None))

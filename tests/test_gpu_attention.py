@@ -245,6 +245,40 @@ def test_page_size_128_block_table(gpu, D):
     _run_and_check(c, f"PS=128 decode D={D}")
 
 
+@pytest.mark.parametrize("M,PS,D,causal", [(300, 16, 128, True), (300, 16, 64, True),
+                                             (200, 24, 128, True), (4, 16, 128, True),
+                                             (4, 16, 128, False), (1, 16, 64, False)])
+def test_q_lens_padding_rows(gpu, M, PS, D, causal):
+    """q_lens: only rows i < q_lens[b] are live (a ragged chunk padded to M
+    rows). Live rows match the oracle; padding rows are zeros even when their
+    Q is NaN. Covers the tile-DMA prefill kernel (PS 16), the register-staged
+    one (PS 24), and the decode kernels (M*group <= 64), with q_lens 0, M and
+    partial tiles."""
+    B, Hq, Hk = 5, 8, 2
+    g = torch.Generator().manual_seed(300 + M + D + PS)
+    q_lens = [M, 0, max(1, M // 3), max(1, M - 1), max(1, (M * 3) // 4)]
+    prior = torch.randint(0, 400, (B,), generator=g).tolist()
+    lengths = [p + n for p, n in zip(prior, q_lens)]
+    lengths[1] = 50                      # keys but no live rows
+    c = _small_paged(B, Hq, Hk, M, lengths, PS=PS, D=D, seed=310 + M + D, causal=causal,
+                     q_offsets=prior if causal else None)
+    for b, n in enumerate(q_lens):
+        c["q"][b, :, n:] = float("nan")  # padding Q must never reach a live output
+    qo = c["q_offsets"]
+    qo_arg = 0 if qo is None else torch.tensor(qo, dtype=torch.int32, device=gpu)
+    ql = torch.tensor(q_lens, dtype=torch.int32, device=gpu)
+    out = flash_attn_paged(c["q"], c["kp"], c["vp"], c["seqlen"], PS, c["hm"], causal, qo_arg, 0,
+                           block_table=c["bt"], q_lens=ql).cpu()
+    qc = c["q"].clone()
+    for b, n in enumerate(q_lens):
+        qc[b, :, n:] = 0.0
+        assert (out[b, :, n:] == 0).all(), f"padding rows of b={b}"
+    ref = paged_reference(qc, c["kp"], c["vp"], c["bt"], lengths, PS, c["hm"], causal, qo)
+    for (b, h), r in ref.items():
+        n = q_lens[b]
+        assert_close(out[b, h, :n].numpy(), r[:n], f"q_lens b={b} h={h}")
+
+
 def test_chunked_prefill_per_sequence_offsets(gpu):
     prior = [0, 37, 150, 600]
     M = 130

@@ -71,8 +71,8 @@ def test_free_returns_pages_and_reset_keeps_the_pool():
 @pytest.mark.parametrize("positions,msg", [
     (torch.tensor([3, 4, 6]), "consecutive"),
     (torch.tensor([1, 2]), "T entries"),
-    (torch.tensor([[0, 1, 2], [5, 6, 8], [0, 1, 2]]), "consecutive"),
     (torch.tensor([[0, 1, 2]]), "match"),
+    (torch.tensor([[0, 1, 2], [5, -6, 8], [0, 1, 2]]), "non-negative"),
     (-1, "non-negative"),
 ])
 def test_positions_validation(positions, msg):
@@ -110,3 +110,101 @@ def test_valid_counts_are_validated():
     k8 = torch.zeros(3, 2, 8, 64, dtype=torch.float16)
     with pytest.raises(ValueError, match="overwrite"):
         c.append(k8, k8, 0, valid=[5, 8, 8])
+
+
+def test_scattered_rows_take_the_scatter_launch():
+    """A [B, T] row that is not consecutive (the reference's general path,
+    engine/llama_tp.py:80-99) maps the pages up to its largest position and
+    goes to the scatter operator, which refuses CPU tensors."""
+    c = _cache()
+    k = torch.zeros(3, 2, 3, 64, dtype=torch.float16)
+    pos = torch.tensor([[0, 1, 2], [40, 6, 8], [2, 1, 0]])
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        c.append(k, k, pos)
+    assert [len(_mapped(c, b)) for b in range(3)] == [1, 3, 1]
+    with pytest.raises(ValueError, match="consecutive positions only"):
+        c.append(k, k, pos, valid=[3, 3, 3])
+
+
+def test_keep_last_of_duplicates():
+    from hrm_flashrenderer_amd.kv_cache import keep_last_of_duplicates
+    pos = np.array([[5, 7, 5, 9, 7], [0, 1, 2, 3, 4], [3, 3, 3, 3, 3]])
+    got = keep_last_of_duplicates(pos)
+    assert got.tolist() == [[-1, -1, 5, 9, 7], [0, 1, 2, 3, 4], [-1, -1, -1, -1, 3]]
+    assert pos[0, 0] == 5   # input untouched
+    # brute force on random rows: each surviving position is the last occurrence
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        row = rng.integers(0, 6, size=(1, 9))
+        got = keep_last_of_duplicates(row)[0]
+        for t in range(9):
+            later = row[0, t + 1:]
+            assert got[t] == (-1 if row[0, t] in later else row[0, t])
+
+
+def test_per_sequence_layout():
+    """layout="per_sequence": the reference's [bsz, Hk, P, PS, D] pages with no
+    block table (engine/llama_tp.py:41-57), grown by doubling with a copy."""
+    c = _cache(layout="per_sequence")
+    assert tuple(c.k_pages.shape) == (3, 2, 2, 16, 64) and c.block_table is None
+    assert c.max_blocks == 2 and c.pool_pages == 6
+    c.k_pages[1, :, 1].fill_(7.0)
+    c.reserve(1, 16 * 3)              # 3 pages: P doubles to 4, contents kept
+    assert tuple(c.k_pages.shape) == (3, 2, 4, 16, 64) and c.max_blocks == 4
+    assert (c.k_pages[1, :, 1] == 7.0).all()
+    c.reserve(0, 16 * 9)              # 9 > 2 * 4 pages
+    assert c.max_blocks == 9
+    c.free(1)
+    assert c.max_blocks == 9 and c.lengths[1] == 0
+    kp, vp, sl = c.get()
+    assert kp is c.k_pages and vp is c.v_pages and sl is c.seqlen
+    with pytest.raises(ValueError, match="layout"):
+        _cache(layout="paged")
+
+
+def test_shared_pool_without_block_table_names_the_fix():
+    """The reference caller passes no block table (engine/llama_tp.py:187-200);
+    on the shared pool with B > 1 the operators say what is missing."""
+    from hrm_flashrenderer_amd.ops import validate_flash_attn_paged, validate_paged_kv_append
+    c = _cache()
+    q = torch.zeros(3, 4, 1, 64, dtype=torch.float16)
+    hm = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match=r"B mismatch: .*block_table="):
+        validate_flash_attn_paged(q, c.k_pages, c.v_pages, c.seqlen, 16, hm,
+                                  require_device=False)
+    assert validate_flash_attn_paged(q, c.k_pages, c.v_pages, c.seqlen, 16, hm,
+                                     block_table=c.block_table, require_device=False) == 2
+    k = torch.zeros(3, 2, 1, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match=r"B mismatch: .*block_table="):
+        validate_paged_kv_append(c.k_pages, c.v_pages, k, k, 0, 16, require_device=False)
+    # a plain size mismatch keeps the reference's bare message
+    kp2 = torch.zeros(2, 2, 2, 16, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match=r"^B mismatch$"):
+        validate_flash_attn_paged(q, kp2, kp2, c.seqlen, 16, hm, require_device=False)
+
+
+def test_chunked_prefill_schedule():
+    """Per-sequence positions: each sequence starts at its cached length and
+    advances chunk by chunk; finished sequences get valid 0."""
+    from hrm_flashrenderer_amd.kv_cache import chunked_prefill_plan, chunked_prefill_schedule
+    sched = chunked_prefill_schedule([700, 130, 0, 256], 256, cached_lengths=[0, 1000, 5, 40])
+    assert sched == [([0, 1000, 5, 40], [256, 130, 0, 256]),
+                     ([256, 1256, 261, 296], [256, 0, 0, 0]),
+                     ([512, 1512, 517, 552], [188, 0, 0, 0])]
+    # without cached prefixes it is the padded plan's chunking, per sequence
+    for (starts, valid), (start, valid2) in zip(chunked_prefill_schedule([700, 130, 0, 256], 256),
+                                                chunked_prefill_plan([700, 130, 0, 256], 256)):
+        assert starts == [start] * 4 and valid == valid2
+    # every prompt token is covered exactly once, at the right position
+    prompts, cached = [513, 1, 77, 0, 300], [3, 0, 900, 12, 64]
+    seen = {b: [] for b in range(5)}
+    for starts, valid in chunked_prefill_schedule(prompts, 128, cached):
+        for b, (s0, n) in enumerate(zip(starts, valid)):
+            seen[b] += list(range(s0, s0 + n))
+    for b in range(5):
+        assert seen[b] == list(range(cached[b], cached[b] + prompts[b]))
+    assert chunked_prefill_schedule([], 64) == []
+    with pytest.raises(ValueError):
+        chunked_prefill_schedule([5], 0)
+    with pytest.raises(ValueError):
+        chunked_prefill_schedule([5, 6], 4, cached_lengths=[1])
