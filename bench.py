@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention path on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,1,tm,gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,4,3,5,5r,1,tm,gemm]
                     [--no-cpu-baseline]
 
 Prints ONE JSON line on stdout (diagnostics go to stderr). The headline
@@ -12,7 +12,8 @@ HBM. The same line carries the decode half of the metric under "decode":
 configuration 4 (Llama-70B shape, B=64, context U[1024,16384], 64/8 heads):
 a step appends one token per sequence and then runs decode attention over the
 full context; decode GB/s counts live K/V + q/o + block-table bytes.
-Configurations 3, 5 and 1 are reported under "extra".
+Configurations 3, 5 and 1 are reported under "extra", with "5r" (cfg5 with
+ragged chunks, timed with and without q_lens).
 
 Per-kernel durations come from HIP events recorded on the stream the kernels
 run on (torch's current stream). `roofline.achieved` is algorithmic work per
@@ -157,7 +158,7 @@ def roofline(bound, work, mean_ms, traffic=None):
 
 # ---------------------------------------------------------------- configs ---
 
-def bench_prefill(w, steps, warmup, traffic_key, traffic):
+def bench_prefill(w, steps, warmup, traffic_key, traffic, q_lens=None):
     flops = workloads.attention_flops(w)
     qo = w.q_offsets if w.q_offsets is not None else 0
     stream = torch.cuda.current_stream()
@@ -166,7 +167,7 @@ def bench_prefill(w, steps, warmup, traffic_key, traffic):
         if ev:
             ev[0].record(stream)
         flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, w.causal, qo,
-                         block_table=w.block_table)
+                         block_table=w.block_table, q_lens=q_lens)
         if ev:
             ev[1].record(stream)
 
@@ -240,6 +241,33 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
         out["append_bytes_per_step"] = abytes
         out["end_to_end_ms"] = round(mean_step, 4)
     return out
+
+
+def bench_decode_rows(w, steps, warmup, rows=(1, 4, 16)):
+    """Paged attention over cfg4's pool with M query rows per sequence (the
+    last M positions, causal: speculative or short-chunk decode). M = 1 and
+    4 take the decode kernels (M * 64/8 heads <= 64); M = 16 (128 rows per
+    KV head) takes the prefill kernel with 16 of its 128 rows live per q head.
+    GB/s counts the live K/V, q/o, block table and seqlen bytes once."""
+    res = {}
+    dev = w.q.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(1204)
+    for M in rows:
+        q = torch.randn(w.B, w.Hq, M, w.D, generator=g, device=dev).half()
+        qo = torch.tensor([n - M for n in w.lengths], dtype=torch.int32, device=dev)
+        nbytes = (sum(w.lengths) * w.Hk * w.D * 4 + 2 * w.B * w.Hq * M * w.D * 2
+                  + sum((n + 15) // 16 for n in w.lengths) * 4 + 4 * w.B)
+
+        def step(ev, q=q, qo=qo):
+            flash_attn_paged(q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True, qo,
+                             block_table=w.block_table)
+
+        _, mean_ms = back_to_back(step, steps, warmup)
+        res[f"M{M}"] = {"kernel_ms_back_to_back": round(mean_ms, 4), "bytes_per_step": nbytes,
+                        "roofline": roofline("hbm", nbytes, mean_ms),
+                        "path": "decode" if M * (w.Hq // w.Hk) <= 64 else "prefill"}
+    return res
 
 
 def bench_gemm_reference(dev, n=8192, iters=20):
@@ -321,6 +349,22 @@ def bench_token_major(steps, warmup, dev, traffic, H=40, KVH=8, Dh=128, t=32767,
 
 # ------------------------------------------------------------ CPU baseline ---
 
+def cpu_threads():
+    """Host threads for the CPU baseline: the CPUs this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when it is set. A one-GPU
+    job on the benchmark box is allotted a share of the host (16 CPUs,
+    OMP_NUM_THREADS=16) although os.cpu_count() reports every core of the
+    machine; more threads than the share would oversubscribe it."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        avail = min(avail, int(omp))
+    return max(1, avail)
+
+
 def cpu_baseline_paged(w, kind, budget_s=10.0):
     """Time the oracle's restatement of the reference CPU path on this host.
 
@@ -331,6 +375,8 @@ def cpu_baseline_paged(w, kind, budget_s=10.0):
     of the decode step is a copy of B rows."""
     from oracle import attention as ora
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     threads = torch.get_num_threads()
     q = w.q.cpu()
     kp, vp = w.k_pool.cpu(), w.v_pool.cpu()
@@ -391,7 +437,9 @@ def cpu_baseline_paged(w, kind, budget_s=10.0):
               + f"; {dt:.2f} s on the host")
     return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port",
             "sample": sample, "extrapolated": heads_done < w.B * w.Hq,
-            "cpu": cpu_info(), "torch": torch.__version__}
+            "cpu_count": os.cpu_count(), "threads_note": "torch intra-op threads = the CPUs "
+            "this process may use (affinity, capped by OMP_NUM_THREADS); cpu_count is the "
+            "whole machine", "cpu": cpu_info(), "torch": torch.__version__}
 
 
 # -------------------------------------------------------------------- main ---
@@ -401,7 +449,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="2,4,3,5,1,tm,gemm")
+    ap.add_argument("--configs", default="2,4,3,5,5r,1,tm,gemm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-mebibyte device buffer --steps times (the reference "
@@ -451,6 +499,10 @@ def main():
         extra["decode_cfg4_rope"] = bench_decode(w4, K, W, "decode_cfg4", traffic, rope=rope)
         log(f"cfg4 with fused rotary embedding: decode "
             f"{extra['decode_cfg4_rope']['roofline']['achieved']} GB/s")
+        extra["decode_cfg4_query_rows"] = bench_decode_rows(w4, K, W)
+        log("cfg4 pool with M query rows: " + ", ".join(
+            f"{k} {v['roofline']['achieved']} GB/s ({v['path']})"
+            for k, v in extra["decode_cfg4_query_rows"].items()))
         if not args.no_cpu_baseline:
             cpu["cfg4"] = cpu_baseline_paged(w4, "bytes")
             log(f"cfg4 cpu: {cpu['cfg4']}")
@@ -473,6 +525,20 @@ def main():
         if not args.no_cpu_baseline:
             cpu["cfg5"] = cpu_baseline_paged(w5, "flops")
         del w5
+    if "5r" in cfgs:
+        log("cfg5 ragged: building workload")
+        w5r = workloads.cfg5_ragged(dev)
+        ks = max(3, K // 4)
+        packed = bench_prefill(w5r, ks, min(W, 2), "prefill_cfg5_ragged", traffic, q_lens=w5r.q_lens)
+        padded = bench_prefill(w5r, ks, min(W, 2), "prefill_cfg5_ragged_padded", traffic)
+        extra["chunked_prefill_cfg5_ragged"] = {
+            "note": "ragged chunks (live rows U[64, 512] of 512): TFLOP/s of the live rows' "
+                    "algorithmic flops, with q_lens (padding rows skipped) and without "
+                    "(padding rows computed)",
+            "packed_q_lens": packed, "padded": padded,
+            "speedup": round(padded["kernel_ms_back_to_back"] / packed["kernel_ms_back_to_back"], 3)}
+        log(f"cfg5 ragged: packed {packed['value']} TFLOP/s, padded {padded['value']} TFLOP/s")
+        del w5r
     if "1" in cfgs:
         extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
     if "gemm" in cfgs:
@@ -514,6 +580,11 @@ def main():
         "config": {"workload": "cfg2_prefill_qwen32b" if "2" in cfgs else "custom",
                    **result.get("workload", {})},
         "roofline": result["roofline"],
+        "traffic_source": {"file": "profiles/traffic.json",
+                           "measured_at": traffic.get("_measured_at"),
+                           "how": "constant from rocprofv3 --pmc FETCH_SIZE x 2 + WRITE_SIZE "
+                                  "per dispatch (scaled by a 1 GiB copy), not measured in "
+                                  "this run"},
         "cpu_baseline": cpu.get("cfg2"),
         "kernel_ms_back_to_back": result.get("kernel_ms_back_to_back"),
         "kernel_ms": result.get("kernel_ms"),

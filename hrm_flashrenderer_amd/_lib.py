@@ -28,20 +28,20 @@ SYMBOLS = (
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P]),
     ("fa_flash_attn_paged_fwd", _I,
      [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _P,
-      _I, _P, _SZ, _P]),
-    ("fa_paged_workspace_bytes", _SZ, [_I, _I, _I, _I, _I, _I, _I]),
+      _I, _I, _P, _SZ, _P]),
+    ("fa_paged_workspace_bytes", _SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
     ("fa_paged_kv_append", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     ("fa_flash_attn_paged_rope_fwd", _I,
      [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _P,
-      _I, _P, _SZ, _P, _P, _I, _P]),
+      _I, _I, _P, _SZ, _P, _P, _I, _P]),
     ("fa_paged_kv_append_rope", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P, _P, _I, _P]),
     ("fa_paged_kv_scatter", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P]),
     ("fa_decode_token_major", _I,
-     [_P, _P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P, _SZ, _P]),
-    ("fa_decode_token_major_workspace_bytes", _SZ, [_I, _I, _I, _I]),
+     [_P, _P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _I, _P, _SZ, _P]),
+    ("fa_decode_token_major_workspace_bytes", _SZ, [_I, _I, _I, _I, _I]),
     ("fa_last_error", ctypes.c_char_p, []),
     ("fa_abi_version", _I, []),
 )

@@ -140,12 +140,12 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
 }
 
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacity_pages,
-                                int page_size) {
+                                int page_size, int heads_per_kv) {
   if (B <= 0 || Hq <= 0 || M <= 0 || Hk <= 0 || !head_dim_ok(D)) return 0;
   if (!fa::use_decode_path(B, M, Hq, Hk)) return 0;
   const int cap = capacity_tokens(capacity_pages < 0 ? 0 : capacity_pages,
                                   page_size < 1 ? 1 : page_size);
-  return fa::plan_decode(B, Hq, M, D, Hk, cap).ws_bytes;
+  return fa::plan_decode(B, Hq, M, D, Hk, cap, heads_per_kv).ws_bytes;
 }
 
 static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
@@ -153,7 +153,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                      int Hq, int M, int D, int NB, int Hk, int P, int causal, int64_t q_offset,
                      int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
                      const int32_t* q_lens, const int32_t* block_table, int max_blocks,
-                     void* workspace,
+                     int heads_per_kv, void* workspace,
                      size_t workspace_bytes, const void* rope_cos, const void* rope_sin,
                      int rope_len, void* stream) {
   if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
@@ -193,7 +193,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
 
   (void)hipGetLastError();
   if (fa::use_decode_path(B, M, Hq, Hk)) {
-    const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N);
+    const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N, heads_per_kv);
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
                   workspace == nullptr ? (size_t)0 : workspace_bytes);
@@ -214,11 +214,12 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
                             int B, int Hq, int M, int D, int NB, int Hk, int P, int causal,
                             int64_t q_offset, int64_t k_offset, const int32_t* q_offsets,
                             const int32_t* k_offsets, const int32_t* q_lens,
-                            const int32_t* block_table, int max_blocks, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            const int32_t* block_table, int max_blocks, int heads_per_kv,
+                            void* workspace, size_t workspace_bytes, void* stream) {
   return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
                    causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
-                   max_blocks, workspace, workspace_bytes, nullptr, nullptr, 0, stream);
+                   max_blocks, heads_per_kv, workspace, workspace_bytes, nullptr, nullptr, 0,
+                   stream);
 }
 
 int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void* v_pages,
@@ -227,14 +228,15 @@ int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void*
                                  int causal, int64_t q_offset, int64_t k_offset,
                                  const int32_t* q_offsets, const int32_t* k_offsets,
                                  const int32_t* q_lens, const int32_t* block_table,
-                                 int max_blocks, void* workspace, size_t workspace_bytes,
-                                 const void* rope_cos, const void* rope_sin, int rope_len,
-                                 void* stream) {
+                                 int max_blocks, int heads_per_kv, void* workspace,
+                                 size_t workspace_bytes, const void* rope_cos,
+                                 const void* rope_sin, int rope_len, void* stream) {
   if (rope_cos == nullptr || rope_sin == nullptr || rope_len <= 0)
     return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
   return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
                    causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
-                   max_blocks, workspace, workspace_bytes, rope_cos, rope_sin, rope_len, stream);
+                   max_blocks, heads_per_kv, workspace, workspace_bytes, rope_cos, rope_sin,
+                   rope_len, stream);
 }
 
 static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
@@ -292,15 +294,26 @@ int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const v
                    positions, block_table, max_blocks, rope_cos, rope_sin, rope_len, stream);
 }
 
-size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max) {
+// Most query heads one KV head serves: the engine's map h % KVH (no head
+// map) gives at most ceil(H / KVH); an explicit head map states its own bound
+// (<= 0: H, no assumption).
+static int token_major_hpk(int H, int KVH, int heads_per_kv, bool engine_map) {
+  if (engine_map) return (H + KVH - 1) / KVH;
+  return heads_per_kv <= 0 || heads_per_kv > H ? H : heads_per_kv;
+}
+
+size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max,
+                                             int heads_per_kv) {
   if (H <= 0 || KVH <= 0 || !head_dim_ok(Dh) || t_max < 0 || t_max >= INT_MAX) return 0;
   if (!fa::use_decode_path(1, 1, H, KVH)) return 0;
-  return fa::plan_decode(1, H, 1, Dh, KVH, t_max + 1).ws_bytes;
+  const int hpk = token_major_hpk(H, KVH, heads_per_kv, false);
+  return fa::plan_decode(1, H, 1, Dh, KVH, t_max + 1, hpk).ws_bytes;
 }
 
 int fa_decode_token_major(float* out, const float* q, const void* k_cache, const void* v_cache,
                           int t, int H, int KVH, int Dh, float scale, const int32_t* head_map,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+                          int heads_per_kv, void* workspace, size_t workspace_bytes,
+                          void* stream) {
   if (H <= 0 || KVH <= 0) return fail(FA_ERR_INVALID, "H and KVH must be positive");
   if (!head_dim_ok(Dh)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
   if (t < 0 || t >= INT_MAX) return fail(FA_ERR_INVALID, "position t out of range");
@@ -342,7 +355,9 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.scale_log2 = scale * fa::kLog2e;
 
   (void)hipGetLastError();
-  const fa::DecodePlan plan = fa::plan_decode(1, H, 1, Dh, KVH, p.N);
+  const fa::DecodePlan plan =
+      fa::plan_decode(1, H, 1, Dh, KVH, p.N,
+                      token_major_hpk(H, KVH, heads_per_kv, head_map == nullptr));
   if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
     return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);

@@ -104,10 +104,12 @@ struct AttnParams {
   // slot = segment + workgroup, segment = b*Hk + hk (see fa_decode.hip)
   float* ws_o;          // [B*Hk + dec_wgs, dec_rows, D]
   float* ws_ml;         // [B*Hk + dec_wgs, dec_rows, 2]  (log2 max, sum)
+                        // row rank * M + i of a slot: query position i of the
+                        // rank-th q head (in head order) that reads the slot's KV head
   int* ws_units;        // [B + 1] units (16-key groups x Hk) before sequence b
   int dec_wgs;          // workgroups of the decode kernel
   int dec_seg_cost;     // units charged per segment start in the decode split (fa_decode.hip)
-  int dec_rows;         // row capacity of a slot: Hq * M
+  int dec_rows;         // row capacity of a slot: heads_per_kv * M
   // optional rotary embedding of Q at load time (nullptr: none): fp16 tables
   // [rope_len, D/2]; query row i of sequence b sits at position q_off(b) + i
   const f16* rope_cos;
@@ -198,7 +200,9 @@ struct DecodePlan {
   size_t ml_bytes;  // partial (max, sum), 256-byte aligned
   size_t ws_bytes;  // total, including the unit prefix
 };
-DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens);
+// heads_per_kv: most q heads one KV head serves (<= 0: Hq, no assumption).
+DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
+                       int heads_per_kv);
 // Workgroups to launch for a plan on the current device (<= plan.wgs), for the
 // decode kernel variant the arguments select.
 int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D);

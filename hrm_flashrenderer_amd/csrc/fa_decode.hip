@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         const int row = e / D;
         const int d = e - row * D;
         const int ri = rc + row;
-        if (ri >= nrows) continue;
+        if (ri >= nrows || ri >= p.dec_rows) continue;  // rows past the slot: NaN in the combine
         const float m0 = s_m[0][row], m1 = s_m[1][row];
         const float mx = fmaxf(m0, m1);
         float lsum = 0.f, osum = 0.f;
@@ -537,9 +537,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           lsum = a0 * s_l[0][row] + a1 * s_l[1][row];
           osum = a0 * s_o[0][row][d] + a1 * s_o[1][row][d];
         }
-        // partial rows are indexed by (q head, query position) of the sequence
-        const int hrow = s_heads[ri / p.M] * p.M + ri % p.M;
-        const int64_t srow = (int64_t)slot * p.dec_rows + hrow;
+        // partial rows are indexed by (rank of the q head among the KV head's
+        // query heads, query position): ri < heads_per_kv * M
+        const int64_t srow = (int64_t)slot * p.dec_rows + ri;
         p.ws_o[srow * D + d] = osum;
         if (d == 0) {
           p.ws_ml[srow * 2 + 0] = mx;
@@ -590,13 +590,25 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   const int b = row / (p.M * p.Hq);
 
   const int hk = p.kv_head(hq);
+  // The decode kernel stores the partial rows of KV head hk's query heads in
+  // head order: row rank(hq) * M + qi of the slot, rank(hq) = number of heads
+  // before hq that read hk. A head map that sends more heads to hk than the
+  // slots hold (heads_per_kv) leaves the heads past it without partials: NaN.
+  int rank = 0;
+  if (hk >= 0) {
+    for (int base = 0; base < hq; base += 64) {
+      const int h2 = base + lane;
+      rank += __popcll(__ballot(h2 < hq && p.kv_head(h2) == hk));
+    }
+  }
+  const int ri = rank * p.M + qi;
   float result[DPW];
   const int kv_len = p.kv_len(b);
   if (qi >= p.q_len(b)) {
     // padding row (q_lens): zeros
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = 0.f;
-  } else if (hk < 0) {
+  } else if (hk < 0 || ri >= p.dec_rows) {
 #pragma unroll
     for (int k = 0; k < DPW; ++k) result[k] = __builtin_nanf("");
   } else if (kv_len == 0) {
@@ -610,7 +622,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     const int US = p.ws_units[b] + hk * G;
     const int UE = US + G;
     const int W = p.dec_wgs;
-    const int64_t rbase = (int64_t)(b * p.Hk + hk) * p.dec_rows + (int64_t)hq * p.M + qi;
+    const int64_t rbase = (int64_t)(b * p.Hk + hk) * p.dec_rows + ri;
     float mx = -INFINITY, lsum = 0.f;
     float acc[DPW];
 #pragma unroll
@@ -768,7 +780,8 @@ int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
   return r > 0 ? std::min(plan.wgs, r) : plan.wgs;
 }
 
-DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens) {
+DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
+                       int heads_per_kv) {
   DecodePlan plan;
   // Workspace capacity: up to 1024 workgroups (FA_DECODE_WGS overrides), but
   // not more than the largest possible number of 16-key groups divided by 8.
@@ -777,7 +790,9 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens)
   int64_t wgs = env_int("FA_DECODE_WGS", 1024);
   wgs = std::min<int64_t>(wgs, std::max<int64_t>(1, max_units / 8));
   plan.wgs = (int)wgs;
-  plan.rows = Hq * M;
+  // a slot holds the rows of one KV head's query heads
+  const int hpk = heads_per_kv <= 0 || heads_per_kv > Hq ? Hq : heads_per_kv;
+  plan.rows = hpk * M;
   const size_t slots = (size_t)B * Hk + (size_t)plan.wgs;
   plan.o_bytes = (slots * plan.rows * D * sizeof(float) + 255) / 256 * 256;
   plan.ml_bytes = (slots * plan.rows * 2 * sizeof(float) + 255) / 256 * 256;

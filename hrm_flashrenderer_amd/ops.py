@@ -34,6 +34,7 @@ behaviour):
 """
 from __future__ import annotations
 
+import weakref
 from typing import Optional, Union
 
 import torch
@@ -126,6 +127,31 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+# (id of a head_map tensor, Hk) -> (weak reference to it, its version counter,
+# the most q heads it sends to one KV head); an entry leaves with its tensor
+_HEADS_PER_KV: dict = {}
+
+
+def heads_per_kv(head_map: torch.Tensor, Hk: int) -> int:
+    """The most query heads `head_map` sends to one KV head (entries outside
+    [0, Hk) are ignored), which sizes the decode workspace. The map is read
+    back once per head-map tensor and remembered until the tensor changes or
+    is freed; callers such as engine/llama_tp.py:145-156 build one map per
+    layer and reuse it on every call."""
+    key = (id(head_map), int(Hk))
+    ver = head_map._version
+    hit = _HEADS_PER_KV.get(key)
+    if hit is not None and hit[0]() is head_map and hit[1] == ver:
+        return hit[2]
+    hm = head_map.detach().to("cpu", torch.int64).view(-1)
+    hm = hm[(hm >= 0) & (hm < Hk)]
+    n = int(torch.bincount(hm, minlength=1).max()) if hm.numel() else 0
+    n = max(1, n)
+    ref = weakref.ref(head_map, lambda _r, k=key: _HEADS_PER_KV.pop(k, None))
+    _HEADS_PER_KV[key] = (ref, ver, n)
+    return n
+
+
 # --------------------------------------------------------------------------
 # custom ops (bodies call the C ABI; fake impls make them traceable)
 # --------------------------------------------------------------------------
@@ -159,20 +185,21 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
                          q_offsets: Optional[torch.Tensor], k_offsets: Optional[torch.Tensor],
                          block_table: Optional[torch.Tensor], rope_cos: Optional[torch.Tensor],
                          rope_sin: Optional[torch.Tensor],
-                         q_lens: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         q_lens: Optional[torch.Tensor] = None,
+                         heads_per_kv: int = 0) -> torch.Tensor:
     lib = _lib.load()
     o = torch.empty_like(q)
     B, Hq, M, D = q.shape
     NB, Hk, P = k_pages.size(0), k_pages.size(1), k_pages.size(2)
     max_blocks = int(block_table.size(1)) if block_table is not None else 0
     cap_pages = max_blocks if block_table is not None else P
-    ws_bytes = lib.fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size)
+    ws_bytes = lib.fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size, heads_per_kv)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with _DeviceScope(q) as stream:
         args = (q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(),
                 page_size, head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P,
                 int(causal), q_offset, k_offset, _ptr(q_offsets), _ptr(k_offsets),
-                _ptr(q_lens), _ptr(block_table), max_blocks, _ptr(ws), ws_bytes)
+                _ptr(q_lens), _ptr(block_table), max_blocks, heads_per_kv, _ptr(ws), ws_bytes)
         if rope_cos is None:
             _lib.check(lib.fa_flash_attn_paged_fwd(*args, stream))
         else:
@@ -183,7 +210,7 @@ def _flash_attn_paged_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.
 
 @_flash_attn_paged_op.register_fake
 def _(q, k_pages, v_pages, seqlen, page_size, head_map, causal, q_offset, k_offset, q_offsets,
-      k_offsets, block_table, rope_cos, rope_sin, q_lens=None):
+      k_offsets, block_table, rope_cos, rope_sin, q_lens=None, heads_per_kv=0):
     return torch.empty_like(q)
 
 
@@ -342,8 +369,9 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
         _check(q_lens.dtype == torch.int32, "q_lens int32 required")
         _check(q_lens.is_contiguous(), "contiguous required")
         _check(q_lens.dim() == 1 and q_lens.numel() == B, "q_lens [B] required")
+    hpk = heads_per_kv(head_map, k_pages.size(1))
     return _flash_attn_paged_op(q, k_pages, v_pages, seqlen, page_size, head_map, bool(causal),
-                                qo, ko, qo_t, ko_t, block_table, cos, sin, q_lens)
+                                qo, ko, qo_t, ko_t, block_table, cos, sin, q_lens, hpk)
 
 
 def validate_paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size,

@@ -22,12 +22,17 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .ops import _DeviceScope, _check
+from .ops import _DeviceScope, _check, heads_per_kv
 
 
-def workspace_bytes(heads: int, kv_heads: int, head_dim: int, t_max: int) -> int:
-    """Workspace of one decode step at any position t <= t_max (0: unsupported)."""
-    return int(_lib.load().fa_decode_token_major_workspace_bytes(heads, kv_heads, head_dim, t_max))
+def workspace_bytes(heads: int, kv_heads: int, head_dim: int, t_max: int,
+                    heads_per_kv_bound: Optional[int] = None) -> int:
+    """Workspace of one decode step at any position t <= t_max (0: unsupported).
+    `heads_per_kv_bound`: the most heads a custom head map sends to one KV head
+    (default: ceil(heads / kv_heads), the engine's map h % KVH)."""
+    hpk = -(-heads // kv_heads) if heads_per_kv_bound is None else int(heads_per_kv_bound)
+    return int(_lib.load().fa_decode_token_major_workspace_bytes(heads, kv_heads, head_dim, t_max,
+                                                                 hpk))
 
 
 def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, t: int,
@@ -62,7 +67,8 @@ def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
         _check(head_map.is_contiguous() and head_map.numel() == H, "head_map [H] required")
     sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
     lib = _lib.load()
-    need = lib.fa_decode_token_major_workspace_bytes(H, KVH, Dh, t)
+    hpk = -(-H // KVH) if head_map is None else heads_per_kv(head_map, KVH)
+    need = lib.fa_decode_token_major_workspace_bytes(H, KVH, Dh, t, hpk)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     else:
@@ -73,6 +79,6 @@ def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
     with _DeviceScope(q) as stream:
         _lib.check(lib.fa_decode_token_major(
             out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), t, H, KVH, Dh,
-            sc, head_map.data_ptr() if head_map is not None else None, workspace.data_ptr(),
-            workspace.numel(), stream))
+            sc, head_map.data_ptr() if head_map is not None else None, hpk,
+            workspace.data_ptr(), workspace.numel(), stream))
     return out

@@ -43,6 +43,8 @@ class PagedWorkload:
     lengths: List[int]              # host copy of seqlen
     q_offsets: Optional[torch.Tensor] = None   # int32 [B] (chunked prefill)
     q_offsets_host: Optional[List[int]] = None
+    q_lens: Optional[torch.Tensor] = None      # int32 [B]: live rows of a ragged chunk
+    q_lens_host: Optional[List[int]] = None
     k_new: Optional[torch.Tensor] = None       # [B, Hk, 1, D] (decode + append)
     v_new: Optional[torch.Tensor] = None
     append_pos: Optional[torch.Tensor] = None  # int32 [B]
@@ -162,6 +164,24 @@ def cfg5(device, B=16, M=512):
                   max_blocks=(32768 + M + PAGE - 1) // PAGE, q_offsets=prior)
 
 
+def cfg5_ragged(device, B=16, M=512):
+    """cfg5 with ragged chunks (the per-sequence chunk schedule's steady state):
+    the same priors as cfg5, but sequence b has only valid_b ~ U[64, M] live
+    rows in its M-row chunk (q_lens), so seqlen_b = prior_b + valid_b. Timed
+    with q_lens (padding rows skipped) and without (padding rows computed),
+    both rated by the live rows' algorithmic flops."""
+    prior = _lengths(5, B, 0, 32768)
+    g = torch.Generator().manual_seed(1105)
+    valid = torch.randint(64, M + 1, (B,), generator=g).tolist()
+    lengths = [p + v for p, v in zip(prior, valid)]
+    w = _paged("cfg5_ragged_chunked_prefill_llama70b", 5, B, 64, 8, 128, M, lengths, True, device,
+               max_blocks=(32768 + M + PAGE - 1) // PAGE, q_offsets=prior)
+    w.q_lens = torch.tensor(valid, dtype=torch.int32, device=device)
+    w.q_lens_host = valid
+    w.meta["live_rows"] = int(sum(valid))
+    return w
+
+
 # ------------------------------------------------------------------ costs ---
 
 def visible_pairs(w: PagedWorkload) -> int:
@@ -169,12 +189,13 @@ def visible_pairs(w: PagedWorkload) -> int:
     tot = 0
     for b, n in enumerate(w.lengths):
         if not w.causal:
-            tot += w.M * n
+            tot += (w.q_lens_host[b] if w.q_lens_host is not None else w.M) * n
             continue
         qo = w.q_offsets_host[b] if w.q_offsets_host is not None else 0
+        rows = w.q_lens_host[b] if w.q_lens_host is not None else w.M
         for_rows = 0
-        # row i sees min(n, qo + i + 1) keys
-        for i in range(w.M):
+        # row i sees min(n, qo + i + 1) keys (rows past q_lens are padding)
+        for i in range(rows):
             for_rows += max(0, min(n, qo + i + 1))
         tot += for_rows
     return tot * w.Hq
@@ -214,6 +235,6 @@ def sample_meta(w: PagedWorkload) -> dict:
                 max_len=int(max(w.lengths)), **w.meta)
 
 
-__all__ = ["PagedWorkload", "cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "attention_flops",
+__all__ = ["PagedWorkload", "cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "cfg5_ragged", "attention_flops",
            "decode_bytes", "append_bytes", "causal_flops_contiguous", "roofline_peaks",
            "visible_pairs", "sample_meta"]

@@ -88,6 +88,13 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
  *              An additive extension for chunked prefill with per-sequence
  *              offsets (the reference's generate loop, engine/llama_tp.py:
  *              338-354, runs equal-length chunks only).
+ *   heads_per_kv : the most query heads head_map sends to one KV head
+ *              (Hq/Hk for the usual GQA map hq // (Hq/Hk)); <= 0 means Hq,
+ *              no assumption. It sizes the decode workspace, whose partial
+ *              slots each hold one KV head's query rows. If head_map sends
+ *              more heads to a KV head, the heads past the bound get NaN rows
+ *              on the decode path (M * ceil(Hq/Hk) <= 64); nothing is written
+ *              out of bounds.
  *   workspace : device scratch of at least fa_paged_workspace_bytes(...)
  *               bytes for the same arguments (may be NULL when that is 0);
  *               its contents need no initialisation.
@@ -100,16 +107,19 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
                             const int32_t* q_offsets, const int32_t* k_offsets,
                             const int32_t* q_lens,
                             const int32_t* block_table, int max_blocks,
+                            int heads_per_kv,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
 /*
- * Workspace bytes fa_flash_attn_paged_fwd needs for these shapes. It depends
- * only on host-known sizes (the per-sequence capacity in pages is P, or
- * max_blocks when a block table is used), never on device contents.
+ * Workspace bytes fa_flash_attn_paged_fwd needs for these shapes and this
+ * heads_per_kv bound. It depends only on host-known sizes (the per-sequence
+ * capacity in pages is P, or max_blocks when a block table is used), never on
+ * device contents: (B*Hk + W) slots x heads_per_kv*M rows x (D + 2) fp32, W
+ * the decode workgroup count (<= 1024), plus B + 1 ints.
  */
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk,
-                                int capacity_pages, int page_size);
+                                int capacity_pages, int page_size, int heads_per_kv);
 
 /*
  * Write T new tokens per sequence into their pages, in place:
@@ -146,6 +156,7 @@ int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void*
                                  const int32_t* q_offsets, const int32_t* k_offsets,
                                  const int32_t* q_lens,
                                  const int32_t* block_table, int max_blocks,
+                                 int heads_per_kv,
                                  void* workspace, size_t workspace_bytes,
                                  const void* rope_cos, const void* rope_sin, int rope_len,
                                  void* stream);
@@ -206,14 +217,20 @@ int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const v
  * of 30-70 already exceeds the 2e-3 + 1e-2|ref| bar). Softmax and the output
  * accumulate in fp32; the softmax weights enter the P.V product as fp16
  * (2^-11 relative each). A head_map entry outside [0, KVH) yields NaN rows.
- * workspace: fa_decode_token_major_workspace_bytes(H, KVH, Dh, t_max) bytes
- * for any t <= t_max (0 when the shape is unsupported).
+ * heads_per_kv: with a head_map, the most heads it sends to one KV head
+ * (<= 0: H); ignored without one (the engine's map: ceil(H / KVH)). Heads
+ * past the bound get NaN rows.
+ * workspace: fa_decode_token_major_workspace_bytes(H, KVH, Dh, t_max,
+ * heads_per_kv) bytes for any t <= t_max (0 when the shape is unsupported);
+ * heads_per_kv = ceil(H / KVH) covers the engine's map.
  */
 int fa_decode_token_major(float* out, const float* q, const void* k_cache, const void* v_cache,
                           int t, int H, int KVH, int Dh, float scale, const int32_t* head_map,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          int heads_per_kv, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
-size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max);
+size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max,
+                                             int heads_per_kv);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* fa_last_error(void);

@@ -62,25 +62,25 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     assert rc == -1 and msg == "fp16 or fp32 required"
     # paged: pool batch must equal B without a block table; page_size positive
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 3, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
-        None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 3, 8, 4, 0, 0, 0, None, None, None, None, 0, 0, None,
+        0, None))
     assert rc == -1 and msg == "B mismatch"
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 0, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
-        None))
+        P, P, P, P, 0, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, 0, None,
+        0, None))
     assert rc == -1 and msg == "page_size mismatch"
     # decode path without its workspace
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None, 0,
-        None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, 0, None,
+        0, None))
     assert rc == -3 and msg.startswith("workspace of")
     rc, msg = _status_and_message(lib.fa_paged_kv_append(
         P, P, P, P, 2, 4, 3, 12, 2, 4, 16, 0, None, None, 0, None))
     assert rc == -1 and msg == "head_dim must be a multiple of 8"
     # rotary variants: tables required; the fused append needs D % 16 == 0
     rc, msg = _status_and_message(lib.fa_flash_attn_paged_rope_fwd(
-        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, None,
-        0, None, None, 0, None))
+        P, P, P, P, 16, P, P, 2, 8, 1, 128, 2, 8, 4, 0, 0, 0, None, None, None, None, 0, 0,
+        None, 0, None, None, 0, None))
     assert rc == -1 and msg == "rotary tables cos/sin [L, D/2] required"
     rc, msg = _status_and_message(lib.fa_paged_kv_append_rope(
         P, P, P, P, 2, 4, 3, 128, 2, 4, 16, 0, None, None, 0, None, None, 0, None))
@@ -102,18 +102,18 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     assert sc(P, P, P, P, 2, 4, 0, 128, 2, 4, 16, None, None, 0, None, None, 0, None) == 0
     # token-major decode (the INT8 engine's cache): shapes, scale, workspace
     tm = lib.fa_decode_token_major
-    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 96, 0.1, None, P, 1 << 20, None))
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 96, 0.1, None, 0, P, 1 << 20, None))
     assert rc == -1 and msg == "Supported head_dim: 64 or 128"
-    rc, msg = _status_and_message(tm(P, P, P, P, 5, 0, 8, 128, 0.1, None, P, 1 << 20, None))
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 0, 8, 128, 0.1, None, 0, P, 1 << 20, None))
     assert rc == -1 and msg == "H and KVH must be positive"
-    rc, msg = _status_and_message(tm(P, P, P, P, -1, 40, 8, 128, 0.1, None, P, 1 << 20, None))
+    rc, msg = _status_and_message(tm(P, P, P, P, -1, 40, 8, 128, 0.1, None, 0, P, 1 << 20, None))
     assert rc == -1 and msg == "position t out of range"
-    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, float("inf"), None, P, 1 << 20,
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, float("inf"), None, 0, P, 1 << 20,
                                      None))
     assert rc == -1 and msg == "scale must be finite"
-    rc, msg = _status_and_message(tm(P, P, None, P, 5, 40, 8, 128, 0.1, None, P, 1 << 20, None))
+    rc, msg = _status_and_message(tm(P, P, None, P, 5, 40, 8, 128, 0.1, None, 0, P, 1 << 20, None))
     assert rc == -1 and msg == "null tensor pointer"
-    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, 0.1, None, P, 16, None))
+    rc, msg = _status_and_message(tm(P, P, P, P, 5, 40, 8, 128, 0.1, None, 0, P, 16, None))
     assert rc == -3 and msg.startswith("workspace of")
     # empty work returns OK without any launch
     assert lib.fa_flash_attn_fwd(P, P, P, P, 0, 0, 8, 8, 16, 16, 64, 1, 0, 0, None, None, None) == 0
@@ -122,25 +122,47 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
 
 def test_workspace_sizing_depends_on_sizes_only():
     lib = _lib.load()
-    # decode (M = 1): partial slots (B*Hk + workgroups) x (Hq*M rows) x (D + 2)
-    # floats (two 256-byte aligned parts) + the (B + 1) unit prefix; 1024
-    # workgroups unless a batch has fewer than 8 groups of 16 keys per workgroup.
-    ws = lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16)
-    slots = 64 * 8 + 1024
+    # decode (M = 1): partial slots (B*Hk + workgroups) x (heads_per_kv*M rows)
+    # x (D + 2) floats (two 256-byte aligned parts) + the (B + 1) unit prefix;
+    # 1024 workgroups unless a batch has fewer than 8 groups of 16 keys per
+    # workgroup. A slot holds one KV head's query rows: cfg4's 64/8 heads need
+    # 8 rows per slot (6.3 MB), against 64 with no bound (50 MB).
     align = lambda x: -(-x // 256) * 256  # noqa: E731
-    assert ws == align(slots * 64 * 128 * 4) + align(slots * 64 * 2 * 4) + 65 * 4
-    small = lib.fa_paged_workspace_bytes(1, 8, 1, 64, 8, 2, 16)  # 16 units -> 2 workgroups
-    assert small == align((8 + 2) * 8 * 64 * 4) + align((8 + 2) * 8 * 2 * 4) + 2 * 4
+    slots = 64 * 8 + 1024
+    for hpk, rows in ((8, 8), (0, 64), (-3, 64), (100, 64), (5, 5)):
+        ws = lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16, hpk)
+        assert ws == align(slots * rows * 128 * 4) + align(slots * rows * 2 * 4) + 65 * 4, hpk
+    assert lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16, 8) < 7_000_000
+    # M = 4 query rows per sequence and 5 heads per KV head: 20 rows per slot
+    ws = lib.fa_paged_workspace_bytes(64, 40, 4, 128, 8, 1025, 16, 5)
+    assert ws == align(slots * 20 * 128 * 4) + align(slots * 20 * 2 * 4) + 65 * 4
+    small = lib.fa_paged_workspace_bytes(1, 8, 1, 64, 8, 2, 16, 1)  # 16 units -> 2 workgroups
+    assert small == align((8 + 2) * 1 * 64 * 4) + align((8 + 2) * 1 * 2 * 4) + 2 * 4
     # prefill-shaped calls need no workspace
-    assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16) == 0
-    assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16) == 0
-    # token-major decode: one sequence of t_max + 1 keys, rows = H
+    assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16, 5) == 0
+    assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16, 1) == 0
+    # token-major decode: one sequence of t_max + 1 keys, rows = heads per KV head
     t_max = 4095  # 256 groups x 8 KV heads = 2048 units -> 256 workgroups
-    ws = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max)
     slots = 8 + 256
-    assert ws == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 2 * 4
-    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100) < ws
-    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max) == 0
+    ws = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 5)
+    assert ws == align(slots * 5 * 128 * 4) + align(slots * 5 * 2 * 4) + 2 * 4
+    ws0 = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 0)   # no bound: H rows
+    assert ws0 == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 2 * 4
+    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100, 5) < ws
+    assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max, 5) == 0
+
+
+def test_heads_per_kv_of_a_head_map():
+    """The bound the Python operators pass: the most q heads one KV head
+    serves, read once per head-map tensor and refreshed when it changes."""
+    from hrm_flashrenderer_amd.ops import heads_per_kv
+    hm = (torch.arange(64) // 8).to(torch.int32)
+    assert heads_per_kv(hm, 8) == 8
+    hm2 = torch.tensor([2, 0, 2, 1, 2, 0], dtype=torch.int32)
+    assert heads_per_kv(hm2, 3) == 3
+    hm2[0] = 1                              # in-place change: read again
+    assert heads_per_kv(hm2, 3) == 2
+    assert heads_per_kv(torch.tensor([5, -1, 7], dtype=torch.int32), 3) == 1  # invalid entries
 
 
 def test_signatures_match_reference():

@@ -356,6 +356,29 @@ def test_arbitrary_head_map(gpu, M):
     _run_and_check(c, "head_map")
 
 
+def test_heads_per_kv_bound_on_the_decode_path(gpu):
+    """The decode workspace holds heads_per_kv * M rows per KV head. A map that
+    sends more heads to a KV head than the bound the caller states gets NaN
+    rows for the heads past it (nothing is written out of bounds); the heads
+    within it stay exact. The public operator derives the bound from the map."""
+    c = _small_paged(2, 6, 3, 1, [700, 260], seed=51, causal=False)
+    c["hm"] = torch.tensor([2, 0, 2, 1, 2, 0], dtype=torch.int32, device=gpu)  # 3 heads on KV 2
+    ref = paged_reference(c["q"], c["kp"], c["vp"], c["bt"], c["lengths"], 16, c["hm"], False)
+    args = (c["q"], c["kp"], c["vp"], c["seqlen"], 16, c["hm"], False, 0, 0, None, None,
+            c["bt"], None, None, None)
+    for bound, nan_heads in ((2, [4]), (1, [2, 4, 5])):
+        out = torch.ops.hrm_fa.flash_attn_paged(*args, bound).cpu().numpy()
+        for (b, h), r in ref.items():
+            if h in nan_heads:
+                assert np.isnan(out[b, h]).all(), f"bound {bound} b={b} h={h}"
+            else:
+                assert_close(out[b, h], r, f"bound {bound} b={b} h={h}")
+    out = flash_attn_paged(c["q"], c["kp"], c["vp"], c["seqlen"], 16, c["hm"], False,
+                           block_table=c["bt"]).cpu().numpy()
+    for (b, h), r in ref.items():
+        assert_close(out[b, h], r, f"derived bound b={b} h={h}")
+
+
 @pytest.mark.parametrize("PS", [128, 24, 8])
 def test_page_sizes_identity_layout(gpu, PS):
     """Reference layout [B, Hk, P, PS, D] without a block table."""
