@@ -29,6 +29,9 @@ SYMBOLS = (
     ("fa_flash_attn_paged_fwd", _I,
      [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _P,
       _I, _I, _P, _SZ, _P]),
+    ("fa_flash_attn_paged_fwd_noalloc", _I,
+     [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _P,
+      _I, _I, _P]),
     ("fa_paged_workspace_bytes", _SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
     ("fa_paged_kv_append", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),

@@ -13,7 +13,19 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
+
+// Decode scratch of fa_flash_attn_paged_fwd_noalloc: the same partial-result
+// workspace that fa_flash_attn_paged_fwd takes from its caller, held in a
+// static device array instead (one copy per GPU, for the life of the
+// process). 32 MiB covers the decode workspace of (B*Hk + 1024) partial
+// slots x 64 rows (e.g. B = 64 sequences of 64/8 heads at M = 8, or B = 2048
+// at M = 1, 8 heads per KV head). In host code `scratch` names a host-side
+// stand-in: only the address from hipGetSymbolAddress (scratch_base) reaches
+// a kernel or a copy.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
 
 namespace {
 
@@ -79,6 +91,28 @@ int check_pool(int B, int NB, int Hk, int P, int page_size, const int32_t* block
   if (block_table == nullptr && NB != B) return fail(FA_ERR_INVALID, "B mismatch");
   if (block_table != nullptr && max_blocks < 0)
     return fail(FA_ERR_INVALID, "block_table [B, max_blocks] required");
+  return FA_OK;
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (hipGetSymbolAddress, with that device current) and kept.
+std::mutex g_scratch_mu;
+void* g_scratch_base[64] = {};
+
+int scratch_base(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(FA_ERR_LAUNCH, "no current HIP device for the static scratch");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_base[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(FA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_base[dev] = ptr;
+  }
+  *out = g_scratch_base[dev];
   return FA_OK;
 }
 
@@ -237,6 +271,33 @@ int fa_flash_attn_paged_rope_fwd(const void* q, const void* k_pages, const void*
                    causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
                    max_blocks, heads_per_kv, workspace, workspace_bytes, rope_cos, rope_sin,
                    rope_len, stream);
+}
+
+int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const void* v_pages,
+                                    const int32_t* seqlen, int page_size,
+                                    const int32_t* head_map, void* o, int B, int Hq, int M,
+                                    int D, int NB, int Hk, int P, int causal, int64_t q_offset,
+                                    int64_t k_offset, const int32_t* q_offsets,
+                                    const int32_t* k_offsets, const int32_t* q_lens,
+                                    const int32_t* block_table, int max_blocks,
+                                    int heads_per_kv, void* stream) {
+  const int cap_pages = block_table != nullptr ? max_blocks : P;
+  const size_t need =
+      fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size, heads_per_kv);
+  if (need > kScratchBytes)
+    return fail(FA_ERR_WORKSPACE,
+                "these shapes need %zu bytes of decode scratch; the allocation-free entry "
+                "holds %zu (call fa_flash_attn_paged_fwd with a workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_base(&ws);
+    if (rc != FA_OK) return rc;
+  }
+  return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
+                   causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
+                   max_blocks, heads_per_kv, ws, need > 0 ? kScratchBytes : 0, nullptr, nullptr,
+                   0, stream);
 }
 
 static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,

@@ -112,6 +112,30 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
                             void* stream);
 
 /*
+ * fa_flash_attn_paged_fwd without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). It has no counterpart in the reference, whose
+ * launcher allocates its output with torch (csrc/flash_attn_sm75.cu:492).
+ * It allocates nothing: the decode path's partial results go to a static
+ * device array of 32 MiB per GPU, held until the process ends. Arguments and
+ * results are those of fa_flash_attn_paged_fwd; shapes whose decode
+ * workspace (fa_paged_workspace_bytes) exceeds 32 MiB are rejected with
+ * FA_ERR_WORKSPACE before anything is launched. All calls on one GPU share
+ * its scratch, so calls that overlap on one GPU (concurrent streams, or
+ * threads without ordering) race; calls ordered on one stream do not. The
+ * scratch needs no initialisation and keeps the last call's contents.
+ */
+int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const void* v_pages,
+                                    const int32_t* seqlen, int page_size,
+                                    const int32_t* head_map, void* o,
+                                    int B, int Hq, int M, int D, int NB, int Hk, int P,
+                                    int causal, int64_t q_offset, int64_t k_offset,
+                                    const int32_t* q_offsets, const int32_t* k_offsets,
+                                    const int32_t* q_lens,
+                                    const int32_t* block_table, int max_blocks,
+                                    int heads_per_kv, void* stream);
+
+/*
  * Workspace bytes fa_flash_attn_paged_fwd needs for these shapes and this
  * heads_per_kv bound. It depends only on host-known sizes (the per-sequence
  * capacity in pages is P, or max_blocks when a block table is used), never on

@@ -31,7 +31,7 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "fa_abi_version", "fa_decode_token_major", "fa_decode_token_major_workspace_bytes",
-        "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd",
+        "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd", "fa_flash_attn_paged_fwd_noalloc",
         "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
         "fa_paged_kv_append_rope", "fa_paged_kv_scatter", "fa_paged_workspace_bytes"])
 

@@ -1,0 +1,92 @@
+"""fa_flash_attn_paged_fwd_noalloc, the entry point that allocates nothing,
+through the C ABI: its outputs must equal fa_flash_attn_paged_fwd's (same
+kernels; the decode partials live in the library's static scratch instead of
+a caller workspace) on two calls in a row, the second smaller than the first
+(the scratch keeps the first call's contents), on a prefill call (no
+scratch), and with a per-call stream; shapes whose workspace exceeds the
+scratch are rejected before any launch."""
+import ctypes
+
+import pytest
+import torch
+
+from hrm_flashrenderer_amd import _lib
+from hrm_flashrenderer_amd.ops import heads_per_kv
+from paged_ref import poison_dead_slots, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(B, Hq, Hk, M, lengths, seed, causal, PS=16):
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(seed)
+    pages = [(n + PS - 1) // PS for n in lengths]
+    total = sum(pages) + 3
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    bt = torch.full((B, max(pages) + 1), -1, dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[pos:pos + n]
+        pos += n
+    kp, vp = seeded((1, Hk, total, PS, 128), seed + 1), seeded((1, Hk, total, PS, 128), seed + 2)
+    poison_dead_slots(kp, vp, bt, lengths, PS)
+    q = seeded((B, Hq, M, 128), seed + 3)
+    return dict(q=q, kp=kp, vp=vp, bt=bt.to(dev), PS=PS, causal=causal,
+                seqlen=torch.tensor(lengths, dtype=torch.int32, device=dev),
+                hm=(torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(dev),
+                qo=torch.tensor([n - M for n in lengths], dtype=torch.int32, device=dev))
+
+
+def _args(c, o):
+    q, kp = c["q"], c["kp"]
+    B, Hq, M, D = q.shape
+    NB, Hk, P = kp.shape[:3]
+    hpk = heads_per_kv(c["hm"], Hk)
+    return ((q.data_ptr(), kp.data_ptr(), c["vp"].data_ptr(), c["seqlen"].data_ptr(), c["PS"],
+             c["hm"].data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P, int(c["causal"]), 0, 0,
+             c["qo"].data_ptr() if c["causal"] else None, None, None, c["bt"].data_ptr(),
+             c["bt"].size(1)), hpk, (B, Hq, M, D, Hk, c["bt"].size(1), c["PS"]))
+
+
+def _both(c):
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    o_ref, o_new = torch.empty_like(c["q"]), torch.empty_like(c["q"])
+    a_ref, hpk, shape = _args(c, o_ref)
+    ws_bytes = lib.fa_paged_workspace_bytes(*shape, hpk)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=c["q"].device)
+    _lib.check(lib.fa_flash_attn_paged_fwd(*a_ref, hpk, ws.data_ptr(), ws_bytes, stream))
+    a_new, _, _ = _args(c, o_new)
+    _lib.check(lib.fa_flash_attn_paged_fwd_noalloc(*a_new, hpk, stream))
+    torch.cuda.synchronize()
+    return o_ref.cpu(), o_new.cpu(), ws_bytes
+
+
+def _same(a, b):
+    return torch.equal(torch.nan_to_num(a, nan=7.0), torch.nan_to_num(b, nan=7.0)) and \
+        torch.equal(torch.isnan(a), torch.isnan(b))
+
+
+def test_no_alloc_entry_matches_the_workspace_entry(gpu):
+    g = torch.Generator().manual_seed(900)
+    big = _case(64, 64, 8, 1, torch.randint(1024, 8192, (64,), generator=g).tolist(), 910, False)
+    small = _case(5, 40, 8, 1, torch.randint(1, 900, (5,), generator=g).tolist(), 920, False)
+    rows4 = _case(7, 16, 4, 4, torch.randint(4, 3000, (7,), generator=g).tolist(), 930, True)
+    prefill = _case(3, 8, 2, 200, [600, 200, 333], 940, True)
+    for name, c in (("decode B=64", big), ("decode B=5 after B=64", small), ("M=4", rows4),
+                    ("prefill", prefill), ("decode B=5 again", small)):
+        ref, new, ws_bytes = _both(c)
+        assert (ws_bytes > 0) == (name != "prefill"), name
+        assert _same(ref, new), name
+        assert torch.isfinite(new).all(), name
+
+
+def test_no_alloc_entry_rejects_shapes_beyond_its_scratch(gpu):
+    lib = _lib.load()
+    P = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    need = lib.fa_paged_workspace_bytes(2048, 64, 8, 128, 8, 2049, 16, 8)
+    assert need > 32 << 20
+    rc = lib.fa_flash_attn_paged_fwd_noalloc(P, P, P, P, 16, P, P, 2048, 64, 8, 128, 1, 8, 40000,
+                                              0, 0, 0, None, None, None, P, 2049, 8, None)
+    msg = lib.fa_last_error().decode()
+    assert rc == -3 and "allocation-free entry holds 33554432" in msg, msg
