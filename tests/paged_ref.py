@@ -20,6 +20,18 @@ def assert_close(out, ref, what=""):
     assert ok, f"{what}: max(|out-ref| - {RTOL}|ref|) = {worst:.3e} > {ATOL}"
 
 
+# The fp32 path (flash_attn with fp32 q/k/v) computes in fp32 throughout, so it
+# is held to a bar two orders tighter: a regression that rounded P to fp16 or
+# used a low-precision exponential (errors of 1e-4..1e-3) fails it.
+ATOL_F32 = 1e-5
+RTOL_F32 = 1e-4
+
+
+def assert_close_f32(out, ref, what=""):
+    ok, worst = ora.within_tolerance(out, ref, ATOL_F32, RTOL_F32)
+    assert ok, f"{what}: max(|out-ref| - {RTOL_F32}|ref|) = {worst:.3e} > {ATOL_F32} (fp32 bar)"
+
+
 def poison_dead_slots(k_pool, v_pool, block_table, lengths, page_size):
     """Write NaN into every pool slot that holds no live token, so a kernel
     that reads past seqlen (or an unmapped page) produces NaN outputs."""

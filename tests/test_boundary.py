@@ -326,3 +326,45 @@ def test_rope_table_validation(rope, msg):
     with pytest.raises(RuntimeError, match=msg):
         ops._check_rope(rope, 128, torch.device("cpu"), require_device=False)
     assert ops._check_rope(None, 128, torch.device("cpu"), require_device=False) == (None, None)
+
+
+def _integration_shim_namespace(real: bool = False):
+    """Executes the `_ext` binding printed in INTEGRATION.md (section 3) against
+    the built library. Unless `real`, it then swaps the shim's library handle
+    for one that fails any compute call, so a test sees whether validation
+    happens first."""
+    text = open(os.path.join(REPO, "INTEGRATION.md")).read()
+    start = text.index("```python\n# flashattention_custom/_ext.py — binds")
+    code = text[start + len("```python\n"):text.index("```", start + 10)]
+    old = os.environ.get("FA_MI355X_LIB")
+    os.environ["FA_MI355X_LIB"] = _lib.LIB_PATH
+    try:
+        ns = {}
+        exec(compile(code, "INTEGRATION.md:_ext.py", "exec"), ns)
+    finally:
+        if old is None:
+            os.environ.pop("FA_MI355X_LIB", None)
+        else:
+            os.environ["FA_MI355X_LIB"] = old
+
+    class NoCompute:
+        def __getattr__(self, name):
+            raise AssertionError(f"C entry {name} reached before validation")
+    if not real:
+        ns["_LIB"] = NoCompute()
+    return ns
+
+
+def test_integration_shim_validates_before_the_c_call():
+    ns = _integration_shim_namespace()
+    q = torch.zeros(1, 8, 16, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="q/k/v must be CUDA"):
+        ns["flash_attn_fwd"](q, q, q)
+    kp = torch.zeros(1, 8, 2, 16, 64, dtype=torch.float16)
+    sl = torch.zeros(1, dtype=torch.int32)
+    hm = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        ns["flash_attn_paged_fwd"](q, kp, kp, sl, 16, hm)
+    k1 = torch.zeros(1, 8, 1, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA required"):
+        ns["paged_kv_append"](kp, kp, k1, k1, 0, 16)

@@ -18,8 +18,8 @@ import torch
 
 from hrm_flashrenderer_amd import flash_attn, flash_attn_paged, paged_kv_append, workloads
 from oracle import attention as ora
-from paged_ref import (assert_close, decode_reference, paged_reference, poison_dead_slots,
-                       seeded)
+from paged_ref import (assert_close, assert_close_f32, decode_reference, paged_reference,
+                       poison_dead_slots, seeded)
 
 pytestmark = pytest.mark.gpu
 
@@ -66,8 +66,9 @@ def test_golden_reference_outputs(gpu):
         causal, qo, ko = g[f"{name}/meta"].tolist()
         q, k, v = (torch.from_numpy(g[f"{name}/{x}"]).to(gpu) for x in "qkv")
         out = flash_attn(q, k, v, bool(causal), qo, ko).cpu()
-        assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), bool(causal), qo, ko), name)
-        assert_close(out, g[f"{name}/o"], name + " vs reference output")
+        check = assert_close_f32 if q.dtype == torch.float32 else assert_close
+        check(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), bool(causal), qo, ko), name)
+        check(out, g[f"{name}/o"], name + " vs reference output")
     for name in ("paged_prefill", "paged_decode", "paged_decode_mha"):
         causal, qo, ko, ps = g[f"{name}/meta"].tolist()
         t = {x: torch.from_numpy(g[f"{name}/{x}"]).to(gpu)
@@ -90,7 +91,8 @@ def test_cfg1_causal_mha(gpu, dtype):
     q, k, v = workloads.cfg1(gpu, dtype)
     out = flash_attn(q, k, v)
     assert out.dtype == dtype and out.shape == q.shape
-    assert_close(out.cpu(), ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True), f"cfg1 {dtype}")
+    check = assert_close_f32 if dtype == torch.float32 else assert_close
+    check(out.cpu(), ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True), f"cfg1 {dtype}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -98,14 +100,15 @@ def test_cfg1_causal_mha(gpu, dtype):
 def test_contiguous_gqa_offsets_noncausal(gpu, dtype, D):
     B, Hq, Hk, M, N = 3, 6, 2, 77, 150
     q, k, v = seeded((B, Hq, M, D), 1, dtype), seeded((B, Hk, N, D), 2, dtype), seeded((B, Hk, N, D), 3, dtype)
+    check = assert_close_f32 if dtype == torch.float32 else assert_close
     for causal, qo, ko in ((True, 0, 0), (True, 73, 0), (False, 0, 0), (True, 5, 9)):
         out = flash_attn(q, k, v, causal, qo, ko).cpu()
-        assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal, qo, ko),
-                     f"{dtype} D={D} causal={causal} qo={qo} ko={ko}")
+        check(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal, qo, ko),
+              f"{dtype} D={D} causal={causal} qo={qo} ko={ko}")
     qo_t = torch.tensor([0, 40, 73], dtype=torch.int32, device=gpu)
     out = flash_attn(q, k, v, True, qo_t, 0).cpu()
-    assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True, [0, 40, 73], 0),
-                 "per-sequence q_offset")
+    check(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True, [0, 40, 73], 0),
+          "per-sequence q_offset")
 
 
 # ----------------------------------------------------------- paged path ----
@@ -356,6 +359,39 @@ def test_arbitrary_head_map(gpu, M):
     _run_and_check(c, "head_map")
 
 
+def test_integration_shim_rejects_bad_dtypes_and_layouts(gpu):
+    """The `_ext` binding of INTEGRATION.md on device tensors: bf16, mixed
+    dtypes and non-contiguous inputs raise the reference's messages before
+    any C call (they would otherwise reach a kernel that reads them as fp16
+    or fp32); a valid call through the real library matches flash_attn."""
+    from test_boundary import _integration_shim_namespace
+    ns = _integration_shim_namespace()
+    q = seeded((1, 8, 64, 64), 700)
+    with pytest.raises(RuntimeError, match="fp16 required"):
+        ns["flash_attn_fwd"](q.bfloat16(), q.bfloat16(), q.bfloat16())
+    with pytest.raises(RuntimeError, match="fp16 required"):
+        ns["flash_attn_fwd"](q, q.float(), q)
+    with pytest.raises(RuntimeError, match="contiguous required"):
+        ns["flash_attn_fwd"](q.transpose(2, 3), q, q)
+    kp = seeded((1, 2, 4, 16, 64), 701)
+    sl = torch.tensor([50], dtype=torch.int32, device=gpu)
+    hm = (torch.arange(8) // 4).to(torch.int32).to(gpu)
+    with pytest.raises(RuntimeError, match="fp16 required"):
+        ns["flash_attn_paged_fwd"](q.float(), kp, kp, sl, 16, hm)
+    with pytest.raises(RuntimeError, match="seqlen int32 required"):
+        ns["flash_attn_paged_fwd"](q, kp, kp, sl.long(), 16, hm)
+    k1 = seeded((1, 2, 1, 64), 702)
+    with pytest.raises(RuntimeError, match="fp16 required"):
+        ns["paged_kv_append"](kp, kp, k1.bfloat16(), k1.bfloat16(), 0, 16)
+    # with the real library: equal to the package's operators
+    real = _integration_shim_namespace(real=True)
+    k, v = seeded((1, 8, 64, 64), 703), seeded((1, 8, 64, 64), 704)
+    assert torch.equal(real["flash_attn_fwd"](q, k, v), flash_attn(q, k, v))
+    q1 = q[:, :, :1].contiguous()
+    assert torch.equal(real["flash_attn_paged_fwd"](q1, kp, kp, sl, 16, hm, False),
+                       flash_attn_paged(q1, kp, kp, sl, 16, hm, False))
+
+
 def test_heads_per_kv_bound_on_the_decode_path(gpu):
     """The decode workspace holds heads_per_kv * M rows per KV head. A map that
     sends more heads to a KV head than the bound the caller states gets NaN
@@ -446,6 +482,39 @@ def test_full_size_decode(gpu, cfg):
     assert_close(out, ref, cfg)
 
 
+def _fp32_reference_all_pairs(w, out, what):
+    """Every (sequence, head) output of a full-size prefill workload against an
+    fp32 softmax reference computed on the GPU (torch fp32 matmuls, explicit
+    causal mask): the BASELINE bar is stated against an fp32 softmax
+    reference. The fp64 oracle checks sampled pairs on the CPU as well."""
+    PS = 16
+    B, Hq, M, D = w.q.shape
+    Hk = w.Hk
+    group = Hq // Hk
+    scale = 1.0 / math.sqrt(D)
+    bt = w.block_table
+    worst = 0.0
+    for b in range(B):
+        n = w.lengths[b]
+        npg = (n + PS - 1) // PS
+        pages = bt[b, :npg].long()
+        kk = w.k_pool[0][:, pages].reshape(Hk, npg * PS, D)[:, :n].float()
+        vv = w.v_pool[0][:, pages].reshape(Hk, npg * PS, D)[:, :n].float()
+        qo = w.q_offsets_host[b] if w.q_offsets_host is not None else 0
+        rows = torch.arange(M, device=w.q.device)[:, None] + qo
+        mask = torch.arange(n, device=w.q.device)[None, :] > rows          # [M, n]
+        for hk in range(Hk):
+            qq = w.q[b, hk * group:(hk + 1) * group].float()               # [group, M, D]
+            sc = torch.matmul(qq, kk[hk].t().contiguous()) * scale          # [group, M, n]
+            sc.masked_fill_(mask, float("-inf"))
+            ref = torch.matmul(torch.softmax(sc, dim=-1), vv[hk])           # [group, M, D]
+            got = out[b, hk * group:(hk + 1) * group].float()
+            err = (got - ref).abs() - 1e-2 * ref.abs()
+            worst = max(worst, float(err.max()))
+            del sc, ref
+    assert worst <= 2e-3, f"{what}: max(|out-ref| - 1e-2|ref|) = {worst:.3e} > 2e-3 (fp32 ref)"
+
+
 def test_full_size_prefill_cfg2_sampled_heads(gpu):
     w = workloads.cfg2(gpu)
     out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True,
@@ -456,6 +525,7 @@ def test_full_size_prefill_cfg2_sampled_heads(gpu):
                           True, None, pairs=pairs)
     for (b, h), r in ref.items():
         assert_close(out[b, h], r, f"cfg2 b={b} h={h}")
+    _fp32_reference_all_pairs(w, torch.from_numpy(out).to(gpu), "cfg2 all 160 pairs")
 
 
 def test_full_size_chunked_prefill_cfg5_sampled_heads(gpu):
@@ -469,6 +539,7 @@ def test_full_size_chunked_prefill_cfg5_sampled_heads(gpu):
                           True, w.q_offsets_host, pairs=pairs)
     for (b, h), r in ref.items():
         assert_close(out[b, h], r, f"cfg5 b={b} h={h}")
+    _fp32_reference_all_pairs(w, torch.from_numpy(out).to(gpu), "cfg5 all 1024 pairs")
 
 
 # -------------------------------------------------- reference call pattern ----
