@@ -262,7 +262,11 @@ __device__ __forceinline__ int split_start(const int* units, int B, int Hk, int 
 // keeps the largest |q'| of the row below 2^15 (e = 0 unless |q| >= 2^15, so
 // a q beyond the fp16 range never becomes inf) and is folded back into the
 // row's score scale.
-template <int D, bool ALIGNED, bool QSPLIT>
+//
+// NBLK (1, 2 or 4): column blocks of 16 query rows served by one pass over
+// the segment's K/V. A KV head with more than 16 * NBLK query rows (heads x
+// positions) is walked once per 16 * NBLK rows.
+template <int D, bool ALIGNED, bool QSPLIT, int NBLK>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
@@ -335,108 +339,127 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     __syncthreads();
     const int nrows = s_count * p.M;
 
-    for (int rc = 0; rc < nrows; rc += kRows) {
-      // This lane's query row (column n of the tiles).
-      const int ridx = rc + n;
-      const bool row_ok = ridx < nrows;
-      const int hq = row_ok ? s_heads[ridx / p.M] : 0;
-      const int qi = row_ok ? ridx % p.M : 0;
-      int row_lim = t_end;  // keys j < row_lim are visible to this row
-      if (p.causal) {
-        int64_t lim = (int64_t)qo + qi - ko + 1;
-        if (lim < row_lim) row_lim = lim < 0 ? 0 : (int)lim;
-      }
-
-      half8 qreg[KSTEPS];
-      half8 qlo[QSPLIT ? KSTEPS : 1];
-      float crow = c;  // score scale of this lane's row (log2 units)
-      const int64_t qrow_off = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 8 * quarter;
-      if constexpr (QSPLIT) {
-        const float* qf = reinterpret_cast<const float*>(p.q);
-        floatx4 x[KSTEPS][2];
-        float amax = 0.f;
+    // NBLK column blocks of 16 query rows share each K/V group load: the K
+    // rows are the A operand of every block's S^T, and the in-lane V^T
+    // operand of every block's O^T.
+    for (int rc0 = 0; rc0 < nrows; rc0 += kRows * NBLK) {
+      int row_lim[NBLK];            // keys j < row_lim are visible to this lane's row
+      bool blk_live[NBLK];          // the block holds at least one query row (uniform)
+      half8 qreg[NBLK][KSTEPS];
+      half8 qlo[NBLK][QSPLIT ? KSTEPS : 1];
+      float crow[NBLK];             // score scale of this lane's row (log2 units)
+      float m_ref[NBLK];            // scaled (log2) reference max of the row
+      float l_run[NBLK];
+      floatx4 acc_o[NBLK][DPL];
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
+      for (int bk = 0; bk < NBLK; ++bk) {
+        // This lane's query row (column n of block bk's tiles).
+        const int rc = rc0 + bk * kRows;
+        blk_live[bk] = rc < nrows;
+        const int ridx = rc + n;
+        const bool row_ok = ridx < nrows;
+        const int hq = row_ok ? s_heads[ridx / p.M] : 0;
+        const int qi = row_ok ? ridx % p.M : 0;
+        row_lim[bk] = t_end;
+        if (p.causal) {
+          int64_t lim = (int64_t)qo + qi - ko + 1;
+          if (lim < row_lim[bk]) row_lim[bk] = lim < 0 ? 0 : (int)lim;
+        }
+        crow[bk] = c;
+        const int64_t qrow_off = (((int64_t)b * p.Hq + hq) * p.M + qi) * D + 8 * quarter;
+        if constexpr (QSPLIT) {
+          const float* qf = reinterpret_cast<const float*>(p.q);
+          floatx4 x[KSTEPS][2];
+          float amax = 0.f;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            x[kk][h] = row_ok ? *reinterpret_cast<const floatx4*>(qf + qrow_off + 32 * kk + 4 * h)
-                              : floatx4{0.f, 0.f, 0.f, 0.f};
+          for (int kk = 0; kk < KSTEPS; ++kk) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(x[kk][h][j]));
+            for (int h = 0; h < 2; ++h) {
+              x[kk][h] = row_ok ? *reinterpret_cast<const floatx4*>(qf + qrow_off + 32 * kk + 4 * h)
+                                : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(x[kk][h][j]));
+            }
           }
-        }
-        // the row's four quarters hold its D values
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        int ex = 0;
-        if (amax >= 32768.f && amax <= 3.0e38f) {
-          (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
-          ex -= 15;                 // amax * 2^-ex in [2^14, 2^15)
-        }
-        const float down = ldexpf(1.f, -ex);
-        crow = c * ldexpf(1.f, ex);
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float v = x[kk][j >> 2][j & 3] * down;
-            const f16 hv = (f16)v;
-            qreg[kk][j] = hv;
-            qlo[kk][j] = (f16)(v - (float)hv);  // v - hv is exact in fp32
+          // the row's four quarters hold its D values
+          amax = fmaxf(amax, __shfl_xor(amax, 16));
+          amax = fmaxf(amax, __shfl_xor(amax, 32));
+          int ex = 0;
+          if (amax >= 32768.f && amax <= 3.0e38f) {
+            (void)frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+            ex -= 15;                 // amax * 2^-ex in [2^14, 2^15)
           }
-        }
-      } else {
+          const float down = ldexpf(1.f, -ex);
+          crow[bk] = c * ldexpf(1.f, ex);
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          qreg[kk] = row_ok ? *reinterpret_cast<const half8*>(qp + qrow_off + 32 * kk)
-                            : half8{0, 0, 0, 0, 0, 0, 0, 0};
+          for (int kk = 0; kk < KSTEPS; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float v = x[kk][j >> 2][j & 3] * down;
+              const f16 hv = (f16)v;
+              qreg[bk][kk][j] = hv;
+              qlo[bk][kk][j] = (f16)(v - (float)hv);  // v - hv is exact in fp32
+            }
+          }
+        } else {
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk) {
+            qreg[bk][kk] = row_ok ? *reinterpret_cast<const half8*>(qp + qrow_off + 32 * kk)
+                                  : half8{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+          if (p.rope_cos != nullptr && row_ok)
+            rope_fragment<KSTEPS, 32>(qreg[bk], p, qo + qi, 8 * quarter);
         }
-        if (p.rope_cos != nullptr && row_ok) rope_fragment<KSTEPS, 32>(qreg, p, qo + qi, 8 * quarter);
+        m_ref[bk] = -INFINITY;
+        l_run[bk] = 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc_o[bk][j] = floatx4{0.f, 0.f, 0.f, 0.f};
       }
-
-      float m_ref = -INFINITY;  // scaled (log2) reference max of the row
-      float l_run = 0.f;
       const half2v ones = half2v{(f16)1.f, (f16)1.f};
-      floatx4 acc_o[DPL];
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
       // One 16-token group: S^T on the matrix cores, online softmax with a lazy
       // reference max (O is rescaled only when the max grows by more than 2^8),
       // then O^T += V^T P^T with the in-lane V transpose.
       auto process = [&](const DecodeRegs<D>& r, int t0) {
-        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+        half4 pb[NBLK];
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qreg[kk],
-                                                     s, 0, 0, 0);
-        }
-        if constexpr (QSPLIT) {
+        for (int bk = 0; bk < NBLK; ++bk) {
+          if (!blk_live[bk]) continue;
+          floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kk = 0; kk < KSTEPS; ++kk) {
-            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]), qlo[kk],
-                                                       s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]),
+                                                       qreg[bk][kk], s, 0, 0, 0);
           }
+          if constexpr (QSPLIT) {
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) {
+              s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[kk]),
+                                                         qlo[bk][kk], s, 0, 0, 0);
+            }
+          }
+          // lane holds tokens t0 + 4*quarter + i of row n
+          float sv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim[bk] ? s[i] : -INFINITY;
+          const float gmax =
+              wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * crow[bk];
+          if (__builtin_amdgcn_ballot_w64(gmax > m_ref[bk] + 8.f) != 0) {
+            const float m_new = fmaxf(m_ref[bk], gmax);
+            const float alpha =
+                m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref[bk] - m_new);
+            l_run[bk] *= alpha;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc_o[bk][j] = acc_o[bk][j] * alpha;
+            m_ref[bk] = m_new;
+          }
+          const float m_use = m_ref[bk] == -INFINITY ? 0.f : m_ref[bk];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            pb[bk][i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], crow[bk], -m_use));
+          l_run[bk] = __builtin_amdgcn_fdot2(half2v{pb[bk][0], pb[bk][1]}, ones, l_run[bk], false);
+          l_run[bk] = __builtin_amdgcn_fdot2(half2v{pb[bk][2], pb[bk][3]}, ones, l_run[bk], false);
         }
-        // lane holds tokens t0 + 4*quarter + i of row n
-        float sv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim ? s[i] : -INFINITY;
-        const float gmax = wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * crow;
-        if (__builtin_amdgcn_ballot_w64(gmax > m_ref + 8.f) != 0) {
-          const float m_new = fmaxf(m_ref, gmax);
-          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-          l_run *= alpha;
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) acc_o[j] = acc_o[j] * alpha;
-          m_ref = m_new;
-        }
-        const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-        half4 pb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], crow, -m_use));
-        l_run = __builtin_amdgcn_fdot2(half2v{pb[0], pb[1]}, ones, l_run, false);
-        l_run = __builtin_amdgcn_fdot2(half2v{pb[2], pb[3]}, ones, l_run, false);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
           const int w = j >> 1;
@@ -449,7 +472,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
             hi = pack_hi(r.v[2][w], r.v[3][w]);
           }
           const half4 a = __builtin_bit_cast(half4, u32x2{lo, hi});
-          acc_o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc_o[j], 0, 0, 0);
+#pragma unroll
+          for (int bk = 0; bk < NBLK; ++bk) {
+            if (blk_live[bk])
+              acc_o[bk][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[bk], acc_o[bk][j], 0, 0, 0);
+          }
         }
       };
 
@@ -482,71 +509,77 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       }
       (void)VW;
 
-      // Merge the 4 waves' states: m is uniform per row, l needs the 4 lanes of
-      // a row summed, O^T[j][r] sits at d = DPL*(4*quarter + r) + j. Waves 2, 3
-      // pass their state to waves 0, 1 (in registers there), which publish the
-      // pair merge; the workgroup then merges the two pairs per element.
-      l_run = wave_sum16x(l_run);
-      const int half = wave & 1;
-      if (wave >= 2) {
-        if (quarter == 0) {
-          s_m[half][n] = m_ref;
-          s_l[half][n] = l_run;
-        }
+      // Merge the 4 waves' states block by block: m is uniform per row, l
+      // needs the 4 lanes of a row summed, O^T[j][r] sits at
+      // d = DPL*(4*quarter + r) + j. Waves 2, 3 pass their state to waves 0,
+      // 1 (in registers there), which publish the pair merge; the workgroup
+      // then merges the two pairs per element.
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
+      for (int bk = 0; bk < NBLK; ++bk) {
+        if (!blk_live[bk]) continue;
+        const int rc = rc0 + bk * kRows;
+        const float l_blk = wave_sum16x(l_run[bk]);
+        const int half = wave & 1;
+        if (wave >= 2) {
+          if (quarter == 0) {
+            s_m[half][n] = m_ref[bk];
+            s_l[half][n] = l_blk;
+          }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s_o[half][n][DPL * (4 * quarter + r) + j] = acc_o[j][r];
-        }
-      }
-      __syncthreads();
-      if (wave < 2) {
-        const float m_o = s_m[half][n];
-        const float mx = fmaxf(m_ref, m_o);
-        const float a = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - mx);
-        const float bsc = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_o - mx);
-        l_run = l_run * a + s_l[half][n] * bsc;
+          for (int j = 0; j < DPL; ++j) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float& x = s_o[half][n][DPL * (4 * quarter + r) + j];
-            x = acc_o[j][r] * a + x * bsc;
+            for (int r = 0; r < 4; ++r) s_o[half][n][DPL * (4 * quarter + r) + j] = acc_o[bk][j][r];
           }
         }
-        // all lanes of the row have read s_m / s_l before they are replaced
-        __builtin_amdgcn_wave_barrier();
-        if (quarter == 0) {
-          s_m[half][n] = mx;
-          s_l[half][n] = l_run;
+        __syncthreads();
+        if (wave < 2) {
+          const float m_o = s_m[half][n];
+          const float mx = fmaxf(m_ref[bk], m_o);
+          const float a = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref[bk] - mx);
+          const float bsc = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_o - mx);
+          const float l_pair = l_blk * a + s_l[half][n] * bsc;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float& x = s_o[half][n][DPL * (4 * quarter + r) + j];
+              x = acc_o[bk][j][r] * a + x * bsc;
+            }
+          }
+          // all lanes of the row have read s_m / s_l before they are replaced
+          __builtin_amdgcn_wave_barrier();
+          if (quarter == 0) {
+            s_m[half][n] = mx;
+            s_l[half][n] = l_pair;
+          }
         }
-      }
-      __syncthreads();
+        __syncthreads();
 
-      for (int e = tid; e < kRows * D; e += kDecodeThreads) {
-        const int row = e / D;
-        const int d = e - row * D;
-        const int ri = rc + row;
-        if (ri >= nrows || ri >= p.dec_rows) continue;  // rows past the slot: NaN in the combine
-        const float m0 = s_m[0][row], m1 = s_m[1][row];
-        const float mx = fmaxf(m0, m1);
-        float lsum = 0.f, osum = 0.f;
-        if (mx != -INFINITY) {
-          const float a0 = __builtin_amdgcn_exp2f(m0 - mx);
-          const float a1 = __builtin_amdgcn_exp2f(m1 - mx);
-          lsum = a0 * s_l[0][row] + a1 * s_l[1][row];
-          osum = a0 * s_o[0][row][d] + a1 * s_o[1][row][d];
+        for (int e = tid; e < kRows * D; e += kDecodeThreads) {
+          const int row = e / D;
+          const int d = e - row * D;
+          const int ri = rc + row;
+          if (ri >= nrows || ri >= p.dec_rows) continue;  // rows past the slot: NaN in the combine
+          const float m0 = s_m[0][row], m1 = s_m[1][row];
+          const float mx = fmaxf(m0, m1);
+          float lsum = 0.f, osum = 0.f;
+          if (mx != -INFINITY) {
+            const float a0 = __builtin_amdgcn_exp2f(m0 - mx);
+            const float a1 = __builtin_amdgcn_exp2f(m1 - mx);
+            lsum = a0 * s_l[0][row] + a1 * s_l[1][row];
+            osum = a0 * s_o[0][row][d] + a1 * s_o[1][row][d];
+          }
+          // partial rows are indexed by (rank of the q head among the KV head's
+          // query heads, query position): ri < heads_per_kv * M
+          const int64_t srow = (int64_t)slot * p.dec_rows + ri;
+          p.ws_o[srow * D + d] = osum;
+          if (d == 0) {
+            p.ws_ml[srow * 2 + 0] = mx;
+            p.ws_ml[srow * 2 + 1] = lsum;
+          }
         }
-        // partial rows are indexed by (rank of the q head among the KV head's
-        // query heads, query position): ri < heads_per_kv * M
-        const int64_t srow = (int64_t)slot * p.dec_rows + ri;
-        p.ws_o[srow * D + d] = osum;
-        if (d == 0) {
-          p.ws_ml[srow * 2 + 0] = mx;
-          p.ws_ml[srow * 2 + 1] = lsum;
-        }
+        __syncthreads();
       }
-      __syncthreads();
     }
 
   };
@@ -722,25 +755,42 @@ int env_int(const char* name, int fallback) {
 
 // The decode kernel variant a call runs: row loads from whole 16-token
 // groups (ALIGNED: pages of a multiple of 16 tokens, or contiguous rows D
-// apart), and the fp32-query split (the token-major entry, which always takes
-// the per-row loads).
+// apart), the fp32-query split (the token-major entry, which always takes
+// the per-row loads and one row block per pass), and the row blocks served
+// per K/V pass: enough 16-row blocks for a KV head's query rows
+// (heads_per_kv * M = dec_rows), up to 4.
 struct DecodeVariant {
   bool aligned;
   bool qsplit;
+  int nblk;
 };
+
+// Row blocks per pass at head size D: four blocks at D = 128 spill (their O
+// accumulators alone take 128 registers beside the K/V ring), so D = 128
+// takes at most two and walks larger groups in passes of 32 rows.
+constexpr int max_row_blocks(int D) { return D == 128 ? 2 : 4; }
 
 DecodeVariant decode_variant(const AttnParams& p) {
   DecodeVariant v;
   v.qsplit = p.q_f32 != 0;
   v.aligned = !v.qsplit && (p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D);
+  const int want = p.dec_rows <= kRows ? 1 : p.dec_rows <= 2 * kRows ? 2 : 4;
+  v.nblk = v.qsplit ? 1 : std::min(want, max_row_blocks(p.kv.D));
   return v;
+}
+
+template <int D, bool ALIGNED>
+const void* decode_fn_rows(int nblk) {
+  constexpr int NB4 = max_row_blocks(D) >= 4 ? 4 : 2;  // D = 128 never asks for 4
+  return nblk == 1 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 1>)
+       : nblk == 2 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 2>)
+                   : reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, NB4>);
 }
 
 template <int D>
 const void* decode_fn(DecodeVariant v) {
-  if (v.qsplit) return reinterpret_cast<const void*>(&decode_kernel<D, false, true>);
-  return v.aligned ? reinterpret_cast<const void*>(&decode_kernel<D, true, false>)
-                   : reinterpret_cast<const void*>(&decode_kernel<D, false, false>);
+  if (v.qsplit) return reinterpret_cast<const void*>(&decode_kernel<D, false, true, 1>);
+  return v.aligned ? decode_fn_rows<D, true>(v.nblk) : decode_fn_rows<D, false>(v.nblk);
 }
 
 int resident_decode_wgs(int D, DecodeVariant var) {
@@ -748,10 +798,11 @@ int resident_decode_wgs(int D, DecodeVariant var) {
   // device (CUs x workgroups per CU), cached per device and kernel variant.
   // Launching exactly this many gives every workgroup its equal share in a
   // single round; a partial second round leaves CUs idle.
-  static std::atomic<int> cache[64][8];
+  static std::atomic<int> cache[64][32];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  const int idx = (D == 128 ? 4 : 0) + (var.qsplit ? 2 : 0) + (var.aligned ? 1 : 0);
+  const int blk = var.nblk == 1 ? 0 : var.nblk == 2 ? 1 : 2;
+  const int idx = (D == 128 ? 16 : 0) + blk * 4 + (var.qsplit ? 2 : 0) + (var.aligned ? 1 : 0);
   int v = cache[dev][idx].load(std::memory_order_relaxed);
   if (v > 0) return v;
   int cus = 0, per_cu = 0;
