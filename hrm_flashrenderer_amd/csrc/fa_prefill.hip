@@ -343,9 +343,9 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 //    all q tiles and heads that share one KV head run on one XCD's L2, longest
 //    rows first. When the (sequence, KV group) pairs divide evenly over the
 //    XCDs, XCD x owns pairs x, x + 8, ... (each XCD gets a share of every
-//    sequence length), runs them longest sequence first, two at a time with
-//    their items interleaved, longest q tile first across both, which
-//    shortens the tail.
+//    sequence length) and runs them longest sequence first: four at a time
+//    with their items interleaved when four pairs' K/V fit the L2, otherwise
+//    one after another with only the last two interleaved (see the kernel).
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
@@ -613,22 +613,45 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
     // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
     // x + 8, x + 16, ..., so sequences of different lengths spread over all
-    // XCDs. Two pairs at a time run longest q tile first across both: the
-    // XCD's workgroup slots then finish together (a short tail), and the K/V
-    // of two pairs share the XCD's L2.
+    // XCDs.
     const int kp = per_xcd / per_pair;
-    // Pairs interleaved at a time: four when the K/V of four pairs (at the
-    // per-sequence capacity) fit one XCD's 4 MB L2, else two. Measured at the
-    // settled clock: cfg2 (1 MB per pair) +1.5 % with four over two; cfg5
-    // (about 17 MB per pair) -1.5 % with four and -8.5 % with all sixteen.
+    // When the K/V of four pairs (at the per-sequence capacity) fit one XCD's
+    // 4 MB L2 (cfg2: 1 MB per pair), four pairs at a time run longest q tile
+    // first across all four: the XCD's slots finish together and the four
+    // pairs share the L2 (+1.5 % on cfg2 over two at a time). Longer pairs
+    // (cfg5: up to 17 MB each) run one after another, longest q tile first
+    // within each, so a pair's items start together and stream its K/V
+    // through the L2 once; only the XCD's last two pairs interleave, to keep
+    // the tail short. On cfg5 that fetches 1.03x the algorithmic bytes
+    // against 2.0x with every two pairs interleaved, at 0.4-0.6 % of time
+    // (same-process A/B on two boxes); interleaving the last four fetched
+    // 1.22x and lost 1.6 %, and no interleave at all lost 1.0 %.
     const bool four_fit = (int64_t)p.N * D * 2 * 2 * 4 <= ((int64_t)4 << 20);
-    const int gp = (four_fit && kp % 4 == 0) ? 4 : (kp % 2 == 0) ? 2 : 1;
     const int x = slot & 7, l = slot >> 3;
-    const int gsz = gp * per_pair;
-    const int gi = l / gsz, lg = l - gi * gsz;
-    const int band = gp * group;
-    const int r = lg / band, w = lg - r * band;
-    int j = gi * gp + w / group;
+    int r, w, j;
+    if (four_fit && kp % 4 == 0) {
+      const int gsz = 4 * per_pair;
+      const int gi = l / gsz, lg = l - gi * gsz;
+      const int band = 4 * group;
+      r = lg / band;
+      w = lg - r * band;
+      j = gi * 4 + w / group;
+    } else {
+      const int tp = kp >= 2 ? 2 : 1;            // pairs interleaved at the end
+      const int head_items = (kp - tp) * per_pair;
+      if (l < head_items) {
+        j = l / per_pair;
+        const int lg = l - j * per_pair;
+        r = lg / group;
+        w = lg - r * group;
+      } else {
+        const int l2 = l - head_items;
+        const int band = tp * group;
+        r = l2 / band;
+        w = l2 - r * band;
+        j = kp - tp + w / group;
+      }
+    }
     if (p.seqlen != nullptr && p.q_offsets != nullptr && kp > 1 && kp <= 64) {
       // Chunked prefill over cached context: a pair's work grows with its
       // sequence's key count, so the XCD runs its pairs longest first. One
