@@ -351,16 +351,23 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
 constexpr float kRescaleLog2 = 8.f;
 
-__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+// v_max3_f32 without the canonicalising moves fmaxf adds for inputs the
+// compiler cannot prove canonical (MFMA results): the hardware max already
+// treats a quiet NaN input as missing, and no input here is a signalling NaN.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // Max of 16 values as a depth-3 tree of max3 (six independent max3, then two,
 // then one), instead of a dependent chain of eight.
 __device__ __forceinline__ float max16(const floatx16& s) {
-  const float a0 = max3f(s[0], s[1], s[2]), a1 = max3f(s[3], s[4], s[5]);
-  const float a2 = max3f(s[6], s[7], s[8]), a3 = max3f(s[9], s[10], s[11]);
-  const float a4 = max3f(s[12], s[13], s[14]);
-  const float b0 = max3f(a0, a1, a2), b1 = max3f(a3, a4, s[15]);
-  return fmaxf(b0, b1);
+  const float a0 = vmax3(s[0], s[1], s[2]), a1 = vmax3(s[3], s[4], s[5]);
+  const float a2 = vmax3(s[6], s[7], s[8]), a3 = vmax3(s[9], s[10], s[11]);
+  const float a4 = vmax3(s[12], s[13], s[14]);
+  const float b0 = vmax3(a0, a1, a2), b1 = vmax3(a3, a4, s[15]);
+  return vmax3(b0, b1, b1);
 }
 
 // Per-sequence data of the prefill kernels, loaded without a branch on the
@@ -738,8 +745,9 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // LDS byte offsets of the lane's operands. K: row col, logical chunk
   // 2*ks + half_id at chunk ^ swz_k(col); the chunk bits of 2*ks and half_id
   // are disjoint, so the k-step ks offset is kbase ^ (32 * ks). V (transposing
-  // read, d = 32*i + 16*(gq%2) + 4*(sl%4)): likewise vbase ^ (64 * i). Both
-  // are recomputed per tile (one XOR per read) rather than held in registers.
+  // read, d = 32*i + 16*(gq%2) + 4*(sl%4)): likewise vbase ^ (64 * i). All of
+  // them are held in registers for the whole loop rather than recomputed per
+  // tile: the XORs are VALU work the MFMAs wait behind (+4 % on cfg2).
   const int gq = lane >> 4, sl = lane & 15;
   const int vrow = 4 * (gq >> 1) + (sl >> 2);
   int kbase = col * C::ROWB + 16 * (half_id ^ C::swz_k(col));
@@ -749,10 +757,18 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     vbase = TILE + vrow * C::ROWB + 16 * ((d >> 3) ^ C::swz_v(vrow)) + 2 * (d & 7);
   }
 
+  int kofs[KSTEPS], vofs[DBLK];  // operand byte offsets within a K/V stage
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) kofs[ks] = kbase ^ (32 * ks);
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i) vofs[i] = vbase ^ (64 * i);
   floatx16 acc_o[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) acc_o[i] = floatx16{};
   float m_ref = -INFINITY;
+  float neg_m_use = 0.f;  // -(m_ref, or 0 while m_ref is -inf), kept with m_ref
+  // (m_ref + 2^8) / c: a raw score above it needs the rescale (c > 0)
+  float thr_raw = -INFINITY;
   float l_run = 0.f;
   const float c = p.scale_log2;
   const half2v ones = half2v{(f16)1.f, (f16)1.f};
@@ -770,12 +786,11 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     }
     if (k0 >= wave_lim_max) return;
     const char* buf = smem + PB * 2 * TILE;
-    asm volatile("" : "+v"(kbase), "+v"(vbase));  // keep the XORs below in the loop
     int koff[KSTEPS], voff[DBLK];
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) koff[ks] = kbase ^ (32 * ks);
+    for (int ks = 0; ks < KSTEPS; ++ks) koff[ks] = kofs[ks];
 #pragma unroll
-    for (int i = 0; i < DBLK; ++i) voff[i] = vbase ^ (64 * i);
+    for (int i = 0; i < DBLK; ++i) voff[i] = vofs[i];
 
     constexpr int KA = 2;
     floatx16 s0 = floatx16{};
@@ -804,38 +819,40 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
         if (key >= lim) s0[r] = -INFINITY;
       }
     }
+    // The lane's half of the row is tested on its own: the rescale branch,
+    // taken for the whole wave when any lane's half exceeds the threshold,
+    // takes the full row max (both halves agree on m_ref).
     float mx = max16(s0);
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
-                                                       __builtin_bit_cast(uint32_t, mx), false, false);
-      mx = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]),
-                 __builtin_bit_cast(float, (uint32_t)sw[1])) * c;
-    }
-    if (__builtin_amdgcn_ballot_w64(mx > m_ref + kRescaleLog2) != 0) {
+    if (__builtin_amdgcn_ballot_w64(mx > thr_raw) != 0) {
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx),
+                                                         __builtin_bit_cast(uint32_t, mx), false, false);
+        mx = vmax3(__builtin_bit_cast(float, (uint32_t)sw[0]),
+                   __builtin_bit_cast(float, (uint32_t)sw[1]),
+                   __builtin_bit_cast(float, (uint32_t)sw[1])) * c;
+      }
       const float m_new = fmaxf(m_ref, mx);
       const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) acc_o[i] = acc_o[i] * alpha;
       m_ref = m_new;
+      neg_m_use = m_new == -INFINITY ? 0.f : -m_new;
+      thr_raw = (m_new + kRescaleLog2) / c;
     }
-    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
     half8 pb[2];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      pb[0][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[j], c, -m_use));
-      pb[1][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[8 + j], c, -m_use));
+      pb[0][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[j], c, neg_m_use));
+      pb[1][j] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s0[8 + j], c, neg_m_use));
     }
-    // row sum from the fp16 values the PV product uses: two independent
-    // dot2 chains
-    float ps[2] = {0.f, 0.f};
+    // row sum from the fp16 values the PV product uses, one dot2 chain
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
 #pragma unroll
       for (int j = 0; j < 8; j += 2)
-        ps[st] = __builtin_amdgcn_fdot2(half2v{pb[st][j], pb[st][j + 1]}, ones, ps[st], false);
+        l_run = __builtin_amdgcn_fdot2(half2v{pb[st][j], pb[st][j + 1]}, ones, l_run, false);
     }
-    l_run += ps[0] + ps[1];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int m = 0; m < NMF; ++m) {
