@@ -419,9 +419,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            (int)kRsrcWord3);
 }
 
+// One 16-byte-per-lane LDS DMA: M0 holds the wave's LDS destination, the
+// lanes' rows land one after another from there. Issued as inline asm so the
+// compiler does not track it: it puts an `s_waitcnt vmcnt(0)` in front of
+// every ds_read_b64_tr_b16 that follows a DMA it knows of, which would make
+// each wave wait for its next tile's DMA before reading V of the current one.
+// Ordering is explicit instead: every DMA is waited for (vmcnt(0)) before the
+// barrier that precedes the reads of its stage. The `s_nop 0` is the wait
+// state an LDS DMA needs after an SALU write of M0.
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voffset), "s"(r), "{m0}"(m0) : "memory");
 }
 
 template <int D>
@@ -544,6 +553,11 @@ struct SlabTable {
     asm volatile("" : "+s"(first));
     base = first;
     rows = row_finish(p, b, row_load(p, b, first + lane, wave));
+    // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained) as an instruction
+    // the compiler's wait insertion sees: the block-table load is then known
+    // complete on every path out of the refill, so a later reuse of its
+    // register in the tile loop needs no wait there.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
   }
   // Source of tile T (uniform, non-decreasing over the calls) for this wave.
   __device__ QuarterSrc get(const AttnParams& p, int b, int T, int kv_len, int wave, int lane) {
