@@ -426,8 +426,8 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.ws_o = reinterpret_cast<float*>(ws);
   p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
   p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-  p.dec_wgs = fa::decode_launch_wgs(plan, p, Dh);  // per-row loads, fp32 query split
-  p.dec_seg_cost = 0;  // one workgroup per CU: a segment start costs little
+  p.dec_wgs = fa::decode_launch_wgs(plan, p, Dh);  // strided whole-group loads, fp32 query split
+  p.dec_seg_cost = 0;  // B = 1: a workgroup opens at most two segments
   p.dec_rows = plan.rows;
   return launch_status(fa::launch_decode(p, Dh, (hipStream_t)stream));
 }

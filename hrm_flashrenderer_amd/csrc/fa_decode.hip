@@ -48,6 +48,7 @@ constexpr int kDecodeWaves = 4;
 constexpr int kRows = 16;            // query rows per MFMA column block
 constexpr int kMaxHeads = 256;       // q heads scanned per KV head
 constexpr int kMaxBatch = 2048;      // sequences whose unit prefix fits in LDS
+static_assert(kMaxHeads == kDecodeThreads, "the head map is read one head per thread");
 
 __device__ __forceinline__ float wave_max16x(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
@@ -88,23 +89,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            0x00020000);  // raw buffer, dword format (gfx9)
 }
 
-// Per-lane byte offsets of a group's fragments inside its page (loop invariant):
-// K row n, 16-byte chunks 2*quarter + 4*kk; V rows 4*quarter + i, DPL halves at DPL*n.
+// Per-lane byte offsets of a group's fragments from its first row (loop
+// invariant), with consecutive rows `rowb` bytes apart (2*D inside a page or
+// in contiguous K/V, 2*Hk*D in the token-major cache): K row n, 16-byte chunks
+// 2*quarter + 4*kk; V rows 4*quarter + i, DPL halves at DPL*n.
 template <int D>
 struct GroupLane {
   uint32_t k;
   uint32_t v;
-  __device__ GroupLane(int n, int quarter)
-      : k((uint32_t)(n * 2 * D + 16 * quarter)),
-        v((uint32_t)(4 * quarter * 2 * D + 2 * (D / 16) * n)) {}
+  uint32_t rowb;
+  __device__ GroupLane(int n, int quarter, uint32_t row_bytes)
+      : k((uint32_t)n * row_bytes + 16u * (uint32_t)quarter),
+        v(4u * (uint32_t)quarter * row_bytes + (uint32_t)(2 * (D / 16) * n)),
+        rowb(row_bytes) {}
 };
 
 // Loads the K/V fragments of one 16-token group (rows beyond `t_end` or not
 // addressable read as zero, so masked keys never carry NaN garbage into P V).
-// ALIGNED (pages of a multiple of 16 tokens, or contiguous K/V): the group sits
-// in one page, found by one wave-uniform (scalar) lookup; the loads are raw
-// buffer loads from that page whose range covers only the group's valid rows,
-// so rows past t_end come back as zeros with no per-lane address math.
+// ALIGNED (pages of a multiple of 16 tokens, or unpaged K/V: contiguous or
+// token-major rows at a fixed stride): the group's rows are evenly spaced from
+// one wave-uniform (scalar) lookup; the loads are raw buffer loads whose range
+// covers only the group's valid rows, so rows past t_end come back as zeros
+// with no per-lane address math.
 template <int D, bool ALIGNED>
 __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p, const f16* kp,
                                            const f16* vp, int b, int hk, int t0, int t_end,
@@ -118,7 +124,9 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
     // memory and return zeros.
     const int valid = min(16, t_end - t0);
     int64_t off = valid > 0 ? p.kv.row_offset(b, hk, t0) : -1;
-    const uint32_t nbytes = off >= 0 ? (uint32_t)(valid * 2 * D) : 0u;
+    // rows [0, valid): the last valid row ends (valid - 1) * rowb + 2D bytes
+    // in; row `valid` starts at valid * rowb >= that, so it reads as zero
+    const uint32_t nbytes = off >= 0 ? (uint32_t)(valid - 1) * gl.rowb + (uint32_t)(2 * D) : 0u;
     off = off >= 0 ? off : 0;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp + off, nbytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp + off, nbytes);
@@ -128,11 +136,11 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (VW == 4) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, gl.v + i * 2 * D, 0, kStreamHint);
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, gl.v + i * gl.rowb, 0, kStreamHint);
 #pragma unroll
         for (int w = 0; w < 4; ++w) r.v[i][w] = x[w];
       } else {
-        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, gl.v + i * 2 * D, 0, kStreamHint);
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, gl.v + i * gl.rowb, 0, kStreamHint);
 #pragma unroll
         for (int w = 0; w < VW; ++w) r.v[i][w] = x[w];
       }
@@ -273,6 +281,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int VW = DecodeRegs<D>::VW;
   constexpr int OPAD = D + 4;
 
+  __shared__ int s_hmap[kMaxHeads];   // KV head of every query head (-1: none)
   __shared__ int s_heads[kMaxHeads];
   __shared__ int s_count;
   __shared__ int s_units[kMaxBatch + 1];
@@ -292,7 +301,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   const int n = lane & 15;       // MFMA column: query row within the block
   const int quarter = lane >> 4; // 0..3
 
+  // The head map is read once, in the same round trip as the key counts of
+  // the unit prefix (Hq <= kMaxHeads = one head per thread), so a segment's
+  // head scan below reads LDS instead of waiting on memory.
+  const int my_hk = tid < p.Hq ? p.kv_head(tid) : -1;
   unit_prefix(p, s_units, s_part);
+  s_hmap[tid] = my_hk;
+  __syncthreads();
   const int U = s_units[p.B];
   if (w == 0) {
     for (int b = tid; b <= p.B; b += kDecodeThreads) p.ws_units[b] = s_units[b];
@@ -321,12 +336,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     const int t_end = min(kv_lim, g_stop << 4);
     const int g_end = g_stop;
 
+    // Groups g_begin + wave + 4k of the segment go through a ring of RING
+    // register sets: RING - 1 groups are in flight while one is processed.
+    // The first pass's loads leave before the head scan and the Q loads, so
+    // the segment's first K/V bytes are in flight during both.
+    constexpr int RING = 3;
+    DecodeRegs<D> ring[RING];
+    // Row stride: 2D bytes in pages and contiguous K/V; the fp32-query
+    // (token-major) variant reads rows Hk*D apart. A compile-time 2D keeps
+    // the other variants' offsets constant (+0.3 % on cfg4).
+    const uint32_t row_bytes =
+        QSPLIT ? (uint32_t)(2 * (p.kv.paged ? (int64_t)D : p.kv.stride_tok)) : 2u * D;
+    const GroupLane<D> glane(n, quarter, row_bytes);
+    const int g0 = g_begin + wave;
+    // With ALIGNED loads every prefetch is issued unconditionally (groups past
+    // the end read as empty ranges), which keeps the number of loads in flight
+    // the same on every path, so each group waits only for its own loads.
+    auto prefetch = [&]() {
+#pragma unroll
+      for (int i = 0; i < RING - 1; ++i) {
+        const int gi = g0 + i * kDecodeWaves;
+        if (ALIGNED || gi < g_end)
+          load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter, glane);
+      }
+    };
+    prefetch();
+
     // Query heads that read KV head hk (any head_map, not only h / group).
     if (wave == 0) {
       int count = 0;
       for (int base = 0; base < p.Hq; base += 64) {
         const int hq = base + lane;
-        const bool match = hq < p.Hq && p.kv_head(hq) == hk;
+        const bool match = hq < p.Hq && s_hmap[hq] == hk;
         const uint64_t mask = __ballot(match);
         if (match) {
           const int pos = count + __popcll(mask & ((1ull << lane) - 1ull));
@@ -343,6 +384,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     // rows are the A operand of every block's S^T, and the in-lane V^T
     // operand of every block's O^T.
     for (int rc0 = 0; rc0 < nrows; rc0 += kRows * NBLK) {
+      if (rc0 > 0) prefetch();  // a later pass over the same groups
       int row_lim[NBLK];            // keys j < row_lim are visible to this lane's row
       bool blk_live[NBLK];          // the block holds at least one query row (uniform)
       half8 qreg[NBLK][KSTEPS];
@@ -480,21 +522,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         }
       };
 
-      // Groups g_begin + wave + 4k of the segment, through a ring of RING register
-      // sets: RING - 1 groups are in flight while one is processed.
-      constexpr int RING = 3;
-      DecodeRegs<D> ring[RING];
-      const GroupLane<D> glane(n, quarter);
-      const int g0 = g_begin + wave;
-      // With ALIGNED loads every prefetch is issued unconditionally (groups past
-      // the end read as empty ranges), which keeps the number of loads in flight
-      // the same on every path, so each group waits only for its own loads.
-#pragma unroll
-      for (int i = 0; i < RING - 1; ++i) {
-        const int gi = g0 + i * kDecodeWaves;
-        if (ALIGNED || gi < g_end)
-          load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter, glane);
-      }
       for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
 #pragma unroll
         for (int i = 0; i < RING; ++i) {
@@ -754,9 +781,9 @@ int env_int(const char* name, int fallback) {
 }
 
 // The decode kernel variant a call runs: row loads from whole 16-token
-// groups (ALIGNED: pages of a multiple of 16 tokens, or contiguous rows D
-// apart), the fp32-query split (the token-major entry, which always takes
-// the per-row loads and one row block per pass), and the row blocks served
+// groups (ALIGNED: pages of a multiple of 16 tokens, or unpaged rows at a
+// fixed stride whose 16-row span fits a buffer range), the fp32-query split
+// (the token-major entry, one row block per pass), and the row blocks served
 // per K/V pass: enough 16-row blocks for a KV head's query rows
 // (heads_per_kv * M = dec_rows), up to 4.
 struct DecodeVariant {
@@ -773,7 +800,12 @@ constexpr int max_row_blocks(int D) { return D == 128 ? 2 : 4; }
 DecodeVariant decode_variant(const AttnParams& p) {
   DecodeVariant v;
   v.qsplit = p.q_f32 != 0;
-  v.aligned = !v.qsplit && (p.kv.paged ? (p.kv.PS % 16) == 0 : p.kv.stride_tok == p.kv.D);
+  // Unpaged rows D apart (contiguous K/V), or, with the fp32 query split
+  // (whose variant takes the row stride at run time), any stride whose 16-row
+  // span fits a 32-bit buffer range.
+  v.aligned = p.kv.paged ? (p.kv.PS % 16) == 0
+            : v.qsplit   ? p.kv.stride_tok >= p.kv.D && p.kv.stride_tok <= ((int64_t)1 << 24)
+                         : p.kv.stride_tok == p.kv.D;
   const int want = p.dec_rows <= kRows ? 1 : p.dec_rows <= 2 * kRows ? 2 : 4;
   v.nblk = v.qsplit ? 1 : std::min(want, max_row_blocks(p.kv.D));
   return v;
@@ -789,15 +821,21 @@ const void* decode_fn_rows(int nblk) {
 
 template <int D>
 const void* decode_fn(DecodeVariant v) {
-  if (v.qsplit) return reinterpret_cast<const void*>(&decode_kernel<D, false, true, 1>);
+  if (v.qsplit)
+    return v.aligned ? reinterpret_cast<const void*>(&decode_kernel<D, true, true, 1>)
+                     : reinterpret_cast<const void*>(&decode_kernel<D, false, true, 1>);
   return v.aligned ? decode_fn_rows<D, true>(v.nblk) : decode_fn_rows<D, false>(v.nblk);
 }
 
-int resident_decode_wgs(int D, DecodeVariant var) {
-  // Workgroups of the decode kernel that are resident at once on the current
-  // device (CUs x workgroups per CU), cached per device and kernel variant.
-  // Launching exactly this many gives every workgroup its equal share in a
-  // single round; a partial second round leaves CUs idle.
+int decode_grid_wgs(int D, DecodeVariant var) {
+  // One workgroup per CU of the current device (when the variant fits a CU at
+  // all), cached per device and kernel variant: every workgroup takes its
+  // equal share in a single round. Against as many workgroups as are resident
+  // (two per CU for most variants), same process: token-major +7.8 %, cfg3
+  // +2.2 %, cfg4 +1.1 %. Two workgroups on a CU share its memory pipeline
+  // unevenly (the older one is served first), so the younger half ends late,
+  // and each workgroup's prologue and merge are paid over half the units.
+  // A partial second round (e.g. 320 or 384 workgroups) is slower still.
   static std::atomic<int> cache[64][32];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -812,7 +850,7 @@ int resident_decode_wgs(int D, DecodeVariant var) {
     (void)hipGetLastError();
     return 0;
   }
-  v = cus * per_cu;
+  v = per_cu > 0 ? cus : 0;
   if (v > 0) cache[dev][idx].store(v, std::memory_order_relaxed);
   return v;
 }
@@ -827,7 +865,7 @@ bool use_decode_path(int B, int M, int Hq, int Hk) {
 
 int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
   if (getenv("FA_DECODE_WGS") != nullptr) return plan.wgs;
-  const int r = resident_decode_wgs(D, decode_variant(p));
+  const int r = decode_grid_wgs(D, decode_variant(p));
   return r > 0 ? std::min(plan.wgs, r) : plan.wgs;
 }
 
@@ -836,7 +874,7 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
   DecodePlan plan;
   // Workspace capacity: up to 1024 workgroups (FA_DECODE_WGS overrides), but
   // not more than the largest possible number of 16-key groups divided by 8.
-  // The launch uses min(this, the device's resident workgroups).
+  // The launch uses min(this, one workgroup per CU).
   const int64_t max_units = (int64_t)B * Hk * ((capacity_tokens + 15) / 16);
   int64_t wgs = env_int("FA_DECODE_WGS", 1024);
   wgs = std::min<int64_t>(wgs, std::max<int64_t>(1, max_units / 8));
