@@ -177,26 +177,36 @@ __device__ __forceinline__ void load_group(DecodeRegs<D>& r, const AttnParams& p
   }
 }
 
-// Groups (16 keys) of sequence b that some query row can see.
-// Padding rows (q_lens) see no keys, so a sequence without live rows has none.
-__device__ __forceinline__ int visible_groups(const AttnParams& p, int b) {
+// Keys of sequence b that some query row can see: keys j < the returned
+// limit. Padding rows (q_lens) see no keys, so a sequence without live rows
+// has none.
+__device__ __forceinline__ int visible_keys(const AttnParams& p, int b) {
   const int qlen = p.q_len(b);
   int kv_lim = qlen > 0 ? p.kv_len(b) : 0;
   if (p.causal) {
     const int64_t lim = (int64_t)p.q_off(b) + (qlen - 1) - p.k_off(b) + 1;
     if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
   }
-  return kv_lim > 0 ? (kv_lim + 15) >> 4 : 0;
+  return kv_lim > 0 ? kv_lim : 0;
 }
 
+__device__ __forceinline__ int key_groups(int keys) { return (keys + 15) >> 4; }
+
 // s_units[b] = Hk * (visible groups of sequences before b), s_units[B] = total,
-// computed by the whole workgroup (chunked sums + a 256-wide scan).
-__device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, int* s_part) {
+// computed by the whole workgroup (chunked sums + a 256-wide scan). The
+// visible key limit of each sequence is kept in s_keys[b] for the segments,
+// so the key counts are read from memory once per workgroup.
+__device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, int* s_part,
+                                            int* s_keys) {
   const int tid = threadIdx.x;
   const int chunk = (p.B + kDecodeThreads - 1) / kDecodeThreads;
   const int b0 = tid * chunk, b1 = min(p.B, b0 + chunk);
   int sum = 0;
-  for (int b = b0; b < b1; ++b) sum += visible_groups(p, b) * p.Hk;
+  for (int b = b0; b < b1; ++b) {
+    const int keys = visible_keys(p, b);
+    s_keys[b] = keys;
+    sum += key_groups(keys) * p.Hk;
+  }
   s_part[tid] = sum;
   __syncthreads();
   for (int off = 1; off < kDecodeThreads; off <<= 1) {
@@ -208,7 +218,7 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
   int run = tid > 0 ? s_part[tid - 1] : 0;
   for (int b = b0; b < b1; ++b) {
     s_units[b] = run;
-    run += visible_groups(p, b) * p.Hk;
+    run += key_groups(s_keys[b]) * p.Hk;
   }
   if (tid == kDecodeThreads - 1) s_units[p.B] = s_part[kDecodeThreads - 1];
   __syncthreads();
@@ -285,6 +295,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   __shared__ int s_heads[kMaxHeads];
   __shared__ int s_count;
   __shared__ int s_units[kMaxBatch + 1];
+  __shared__ int s_keys[kMaxBatch];      // visible key limit per sequence
   __shared__ int s_part[kDecodeThreads];
   // Wave merge buffers: waves 2 and 3 hand their state to waves 0 and 1, which
   // then publish the pairwise merge (half the LDS of one slot per wave, so four
@@ -305,7 +316,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   // the unit prefix (Hq <= kMaxHeads = one head per thread), so a segment's
   // head scan below reads LDS instead of waiting on memory.
   const int my_hk = tid < p.Hq ? p.kv_head(tid) : -1;
-  unit_prefix(p, s_units, s_part);
+  unit_prefix(p, s_units, s_part, s_keys);
   s_hmap[tid] = my_hk;
   __syncthreads();
   const int U = s_units[p.B];
@@ -324,16 +335,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 
   // One (b, hk) segment, groups [g_begin, g_end).
   auto segment = [&](int b, int hk, int g_begin, int g_stop, int slot) {
-    const int kv_len = p.kv_len(b);
-    const int qo = p.q_off(b);
-    const int ko = p.k_off(b);
-    const int qlen = p.q_len(b);
-    int kv_lim = kv_len;
-    if (p.causal) {
-      int64_t lim = (int64_t)qo + (qlen - 1) - ko + 1;
-      if (lim < kv_lim) kv_lim = lim < 0 ? 0 : (int)lim;
-    }
-    const int t_end = min(kv_lim, g_stop << 4);
+    // The key limit comes from LDS; the offsets are read only where a row
+    // needs them (causal limits, rotary positions).
+    const int qo = p.causal || p.rope_cos != nullptr ? p.q_off(b) : 0;
+    const int ko = p.causal ? p.k_off(b) : 0;
+    const int t_end = min(s_keys[b], g_stop << 4);
     const int g_end = g_stop;
 
     // Groups g_begin + wave + 4k of the segment go through a ring of RING
