@@ -9,38 +9,57 @@
 // cache, engine/llama_tp.py:80-99), token t of sequence b goes to
 // positions[b*T + t] instead; negative positions are skipped.
 //
+// Each lane's source loads are issued first (every index below total_chunks is
+// in bounds), so their round trip overlaps the dependent position and
+// block-table loads that give the destination.
+//
 // Layout of the work: one lane moves one 16-byte chunk (8 fp16) of K and the
 // same chunk of V. Consecutive lanes take consecutive chunks of a token row,
 // then consecutive tokens, so both the source rows [B,Hk,T,D] and the
 // destination slots (consecutive within a page) are written as whole 64-byte
 // segments per quarter-wave. Work is split as (b, hk, t, chunk); when the chunk
 // count D/8 is a power of two (D = 64, 128) the chunk index is a mask and a
-// shift, otherwise a division.
+// shift, otherwise a division. The index arithmetic is 32-bit (I = uint32_t)
+// whenever the lane count fits, since 64-bit division is a long software
+// sequence ahead of every load; the 64-bit form serves larger appends.
 #include "fa_common.h"
 
 namespace fa {
 
+// row = (b*Hk + hk)*T + t
+template <typename I>
+__device__ __forceinline__ void split_row(I row, int T, int Hk, int& b, int& hk, int& t) {
+  const I bh = row / (I)T;
+  t = (int)(row - bh * (I)T);
+  const I bq = bh / (I)Hk;
+  hk = (int)(bh - bq * (I)Hk);
+  b = (int)bq;
+}
+
+template <typename I>
 __global__ __launch_bounds__(256) void paged_append_kernel(
     f16* __restrict__ k_pages, f16* __restrict__ v_pages,
     const f16* __restrict__ k_new, const f16* __restrict__ v_new,
     KVMap map, int B, int Hk, int T, int chunks_per_row, int chunk_shift, int start_pos,
     const int32_t* __restrict__ start_positions, const int32_t* __restrict__ token_positions,
     int64_t total_chunks) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total_chunks) return;
+  const I idx = (I)blockIdx.x * (I)blockDim.x + (I)threadIdx.x;
+  if ((int64_t)idx >= total_chunks) return;
   int chunk;
-  int64_t row;  // (b*Hk + hk)*T + t
+  I row;
   if (chunk_shift >= 0) {
-    chunk = (int)(idx & ((1 << chunk_shift) - 1));
+    chunk = (int)(idx & (I)((1 << chunk_shift) - 1));
     row = idx >> chunk_shift;
   } else {
-    row = idx / chunks_per_row;
-    chunk = (int)(idx - row * chunks_per_row);
+    row = idx / (I)chunks_per_row;
+    chunk = (int)(idx - row * (I)chunks_per_row);
   }
-  const int t = (int)(row % T);
-  const int64_t bh = row / T;
-  const int hk = (int)(bh % Hk);
-  const int b = (int)(bh / Hk);
+  int b, hk, t;
+  split_row<I>(row, T, Hk, b, hk, t);
+
+  const int64_t src = (int64_t)row * map.D + chunk * 8;
+  const u32x4 kv = *reinterpret_cast<const u32x4*>(k_new + src);
+  const u32x4 vv = *reinterpret_cast<const u32x4*>(v_new + src);
 
   const int pos = token_positions ? token_positions[(int64_t)b * T + t]
                                   : (start_positions ? start_positions[b] : start_pos) + t;
@@ -48,10 +67,7 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
   const int64_t dst_row = map.row_offset(b, hk, pos);
   if (dst_row < 0) return;
 
-  const int64_t src = row * map.D + chunk * 8;
   const int64_t dst = dst_row + chunk * 8;
-  const u32x4 kv = *reinterpret_cast<const u32x4*>(k_new + src);
-  const u32x4 vv = *reinterpret_cast<const u32x4*>(v_new + src);
   *reinterpret_cast<u32x4*>(k_pages + dst) = kv;
   *reinterpret_cast<u32x4*>(v_pages + dst) = vv;
 }
@@ -61,6 +77,7 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
 // the 8-element chunk c < D/16 of a row together with its rotary partner
 // c + D/16: it rotates and writes both K chunks and copies both V chunks.
 // A position outside the rotary table writes NaN keys.
+template <typename I>
 __global__ __launch_bounds__(256) void paged_append_rope_kernel(
     f16* __restrict__ k_pages, f16* __restrict__ v_pages,
     const f16* __restrict__ k_new, const f16* __restrict__ v_new,
@@ -68,26 +85,26 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
     const int32_t* __restrict__ start_positions, const int32_t* __restrict__ token_positions,
     const f16* __restrict__ rope_cos,
     const f16* __restrict__ rope_sin, int rope_len, int64_t total_pairs) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total_pairs) return;
-  const int64_t row = idx / pairs_per_row;
-  const int pair = (int)(idx - row * pairs_per_row);
-  const int t = (int)(row % T);
-  const int64_t bh = row / T;
-  const int hk = (int)(bh % Hk);
-  const int b = (int)(bh / Hk);
+  const I idx = (I)blockIdx.x * (I)blockDim.x + (I)threadIdx.x;
+  if ((int64_t)idx >= total_pairs) return;
+  const I row = idx / (I)pairs_per_row;
+  const int pair = (int)(idx - row * (I)pairs_per_row);
+  int b, hk, t;
+  split_row<I>(row, T, Hk, b, hk, t);
+
+  const int half = map.D / 2;
+  const int64_t src = (int64_t)row * map.D + pair * 8;
+  const half8 x1 = *reinterpret_cast<const half8*>(k_new + src);
+  const half8 x2 = *reinterpret_cast<const half8*>(k_new + src + half);
+  const u32x4 v1 = *reinterpret_cast<const u32x4*>(v_new + src);
+  const u32x4 v2 = *reinterpret_cast<const u32x4*>(v_new + src + half);
 
   const int pos = token_positions ? token_positions[(int64_t)b * T + t]
                                   : (start_positions ? start_positions[b] : start_pos) + t;
   if (pos < 0) return;
   const int64_t dst_row = map.row_offset(b, hk, pos);
   if (dst_row < 0) return;
-
-  const int half = map.D / 2;
-  const int64_t src = row * map.D + pair * 8;
   const int64_t dst = dst_row + pair * 8;
-  const half8 x1 = *reinterpret_cast<const half8*>(k_new + src);
-  const half8 x2 = *reinterpret_cast<const half8*>(k_new + src + half);
   const bool ok = pos < rope_len;
   const int64_t trow = (int64_t)(ok ? pos : 0) * half + pair * 8;
   const half8 c = *reinterpret_cast<const half8*>(rope_cos + trow);
@@ -102,8 +119,8 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
   }
   *reinterpret_cast<half8*>(k_pages + dst) = y1;
   *reinterpret_cast<half8*>(k_pages + dst + half) = y2;
-  *reinterpret_cast<u32x4*>(v_pages + dst) = *reinterpret_cast<const u32x4*>(v_new + src);
-  *reinterpret_cast<u32x4*>(v_pages + dst + half) = *reinterpret_cast<const u32x4*>(v_new + src + half);
+  *reinterpret_cast<u32x4*>(v_pages + dst) = v1;
+  *reinterpret_cast<u32x4*>(v_pages + dst + half) = v2;
 }
 
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
@@ -117,7 +134,9 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
     const int64_t total = (int64_t)B * Hk * T * pairs_per_row;
     if (total == 0) return hipSuccess;
     const int64_t blocks = (total + threads - 1) / threads;
-    hipLaunchKernelGGL(paged_append_rope_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
+    auto fn = total + threads < ((int64_t)1 << 31) ? paged_append_rope_kernel<uint32_t>
+                                                   : paged_append_rope_kernel<int64_t>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), 0, stream,
                        reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
                        reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new),
                        map, B, Hk, T, pairs_per_row, start_pos, start_positions,
@@ -131,7 +150,9 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
   const int64_t total = (int64_t)B * Hk * T * chunks_per_row;
   if (total == 0) return hipSuccess;
   const int64_t blocks = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(paged_append_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream,
+  auto fn = total + threads < ((int64_t)1 << 31) ? paged_append_kernel<uint32_t>
+                                                 : paged_append_kernel<int64_t>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), 0, stream,
                      reinterpret_cast<f16*>(k_pages), reinterpret_cast<f16*>(v_pages),
                      reinterpret_cast<const f16*>(k_new), reinterpret_cast<const f16*>(v_new), map,
                      B, Hk, T, chunks_per_row, chunk_shift, start_pos, start_positions,
