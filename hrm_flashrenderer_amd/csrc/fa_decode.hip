@@ -193,12 +193,16 @@ __device__ __forceinline__ int visible_keys(const AttnParams& p, int b) {
 __device__ __forceinline__ int key_groups(int keys) { return (keys + 15) >> 4; }
 
 // s_units[b] = Hk * (visible groups of sequences before b), s_units[B] = total,
-// computed by the whole workgroup (chunked sums + a 256-wide scan). The
-// visible key limit of each sequence is kept in s_keys[b] for the segments,
-// so the key counts are read from memory once per workgroup.
+// computed by the whole workgroup: each thread sums a chunk of sequences, a
+// shuffle scan within each wave and one exchange of the four wave totals give
+// the prefix (two barriers, against seventeen for a 256-wide LDS scan: the
+// unit prefix is the first thing every workgroup does). The visible key limit
+// of each sequence is kept in s_keys[b] for the segments, so the key counts
+// are read from memory once per workgroup.
 __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, int* s_part,
                                             int* s_keys) {
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int chunk = (p.B + kDecodeThreads - 1) / kDecodeThreads;
   const int b0 = tid * chunk, b1 = min(p.B, b0 + chunk);
   int sum = 0;
@@ -207,20 +211,22 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
     s_keys[b] = keys;
     sum += key_groups(keys) * p.Hk;
   }
-  s_part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < kDecodeThreads; off <<= 1) {
-    const int v = tid >= off ? s_part[tid - off] : 0;
-    __syncthreads();
-    s_part[tid] += v;
-    __syncthreads();
+  int incl = sum;  // inclusive prefix of the chunk sums within the wave
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
   }
-  int run = tid > 0 ? s_part[tid - 1] : 0;
+  if (lane == 63) s_part[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_part[w];
+  int run = base + incl - sum;
   for (int b = b0; b < b1; ++b) {
     s_units[b] = run;
     run += key_groups(s_keys[b]) * p.Hk;
   }
-  if (tid == kDecodeThreads - 1) s_units[p.B] = s_part[kDecodeThreads - 1];
+  if (tid == kDecodeThreads - 1) s_units[p.B] = base + incl;
   __syncthreads();
 }
 
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   __shared__ int s_count;
   __shared__ int s_units[kMaxBatch + 1];
   __shared__ int s_keys[kMaxBatch];      // visible key limit per sequence
-  __shared__ int s_part[kDecodeThreads];
+  __shared__ int s_part[kDecodeWaves];
   // Wave merge buffers: waves 2 and 3 hand their state to waves 0 and 1, which
   // then publish the pairwise merge (half the LDS of one slot per wave, so four
   // workgroups fit on a CU).
