@@ -243,10 +243,10 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
     return out
 
 
-def bench_decode_rows(w, steps, warmup, rows=(1, 4, 16)):
+def bench_decode_rows(w, steps, warmup, rows=(1, 4, 8, 16)):
     """Paged attention over cfg4's pool with M query rows per sequence (the
-    last M positions, causal: speculative or short-chunk decode). M = 1 and
-    4 take the decode kernels (M * 64/8 heads <= 64); M = 16 (128 rows per
+    last M positions, causal: speculative or short-chunk decode). M = 1, 4
+    and 8 take the decode kernels (M * 64/8 heads <= 64); M = 16 (128 rows per
     KV head) takes the prefill kernel with 16 of its 128 rows live per q head.
     GB/s counts the live K/V, q/o, block table and seqlen bytes once."""
     res = {}

@@ -352,7 +352,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     // register sets: RING - 1 groups are in flight while one is processed.
     // The first pass's loads leave before the head scan and the Q loads, so
     // the segment's first K/V bytes are in flight during both.
-    constexpr int RING = 3;
+    // Four blocks at D = 128 compute four times as long per group, so one
+    // group in flight covers the load latency and keeps the accumulators in
+    // registers.
+    constexpr int RING = NBLK >= 4 && D == 128 ? 2 : 3;
     DecodeRegs<D> ring[RING];
     // Row stride: 2D bytes in pages and contiguous K/V; the fp32-query
     // (token-major) variant reads rows Hk*D apart. A compile-time 2D keeps
@@ -804,10 +807,11 @@ struct DecodeVariant {
   int nblk;
 };
 
-// Row blocks per pass at head size D: four blocks at D = 128 spill (their O
-// accumulators alone take 128 registers beside the K/V ring), so D = 128
-// takes at most two and walks larger groups in passes of 32 rows.
-constexpr int max_row_blocks(int D) { return D == 128 ? 2 : 4; }
+// Row blocks per pass: four (64 rows), except the per-row load variant at
+// D = 128, whose four blocks spill; it walks larger groups in passes of 32
+// rows. At D = 128 the four-block variant keeps one 16-key group in flight
+// per wave (their O accumulators alone take 128 registers).
+constexpr int max_row_blocks(int D, bool aligned) { return D == 128 && !aligned ? 2 : 4; }
 
 DecodeVariant decode_variant(const AttnParams& p) {
   DecodeVariant v;
@@ -819,13 +823,13 @@ DecodeVariant decode_variant(const AttnParams& p) {
             : v.qsplit   ? p.kv.stride_tok >= p.kv.D && p.kv.stride_tok <= ((int64_t)1 << 24)
                          : p.kv.stride_tok == p.kv.D;
   const int want = p.dec_rows <= kRows ? 1 : p.dec_rows <= 2 * kRows ? 2 : 4;
-  v.nblk = v.qsplit ? 1 : std::min(want, max_row_blocks(p.kv.D));
+  v.nblk = v.qsplit ? 1 : std::min(want, max_row_blocks(p.kv.D, v.aligned));
   return v;
 }
 
 template <int D, bool ALIGNED>
 const void* decode_fn_rows(int nblk) {
-  constexpr int NB4 = max_row_blocks(D) >= 4 ? 4 : 2;  // D = 128 never asks for 4
+  constexpr int NB4 = max_row_blocks(D, ALIGNED) >= 4 ? 4 : 2;
   return nblk == 1 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 1>)
        : nblk == 2 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 2>)
                    : reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, NB4>);

@@ -352,21 +352,24 @@ def test_decode_few_rows(gpu, M, causal):
     _run_and_check(c, f"M={M}")
 
 
-@pytest.mark.parametrize("Hq,Hk,M,D,causal", [
-    (64, 8, 4, 128, True),    # 32 rows per KV head: two row blocks in one K/V pass
-    (64, 8, 8, 128, False),   # 64 rows at D=128: two passes of two blocks
-    (40, 8, 5, 128, True),    # 25 rows: the second block half empty
-    (32, 4, 8, 64, True),     # 64 rows at D=64: four blocks in one pass
-    (16, 4, 12, 64, False),   # 48 rows: three live blocks of four
+@pytest.mark.parametrize("Hq,Hk,M,D,causal,ps", [
+    (64, 8, 4, 128, True, 16),    # 32 rows per KV head: two row blocks in one K/V pass
+    (64, 8, 8, 128, False, 16),   # 64 rows at D=128: four blocks in one pass
+    (40, 8, 7, 128, True, 16),    # 35 rows: three live blocks of four
+    (40, 8, 5, 128, True, 16),    # 25 rows: the second block half empty
+    (64, 8, 8, 128, True, 24),    # per-row loads (page size 24): two passes of two blocks
+    (32, 4, 8, 64, True, 16),     # 64 rows at D=64: four blocks in one pass
+    (16, 4, 12, 64, False, 16),   # 48 rows: three live blocks of four
 ])
-def test_decode_row_blocks_per_pass(gpu, Hq, Hk, M, D, causal):
-    """The decode kernels serve up to 2 (D=128) or 4 (D=64) blocks of 16 query
-    rows per pass over a KV head's pages; every head of every sequence is
-    checked, with ragged lengths (one empty) and NaN-poisoned dead slots."""
+def test_decode_row_blocks_per_pass(gpu, Hq, Hk, M, D, causal, ps):
+    """The decode kernels serve up to 4 blocks of 16 query rows per pass over a
+    KV head's pages (2 with per-row loads at D=128, which walk larger groups in
+    passes); every head of every sequence is checked, with ragged lengths (one
+    empty) and NaN-poisoned dead slots."""
     lengths = [700, 0, 1500, 33, 2100]
-    c = _small_paged(5, Hq, Hk, M, lengths, D=D, seed=330 + M + D, causal=causal,
+    c = _small_paged(5, Hq, Hk, M, lengths, PS=ps, D=D, seed=330 + M + D, causal=causal,
                      q_offsets=[max(0, n - M) for n in lengths] if causal else None)
-    _run_and_check(c, f"row blocks Hq={Hq} Hk={Hk} M={M} D={D}")
+    _run_and_check(c, f"row blocks Hq={Hq} Hk={Hk} M={M} D={D} PS={ps}")
 
 
 @pytest.mark.parametrize("M", [1, 200])
