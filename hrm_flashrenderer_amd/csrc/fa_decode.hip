@@ -245,27 +245,58 @@ __device__ __forceinline__ int split_cost_p(const AttnParams& p, int U, int W) {
   return U >= 2 * W ? min(p.dec_seg_cost, U / (2 * W)) : 0;
 }
 
-// Smallest unit u whose cost is at least floor(w * C / W); U for w == W.
-__device__ __forceinline__ int split_start(const int* units, int B, int Hk, int U, int W, int P,
-                                           int w) {
+// floor(x * y / z) for 0 <= x * y < 2^63, z > 0: a 32-bit division when the
+// operands fit (the 64-bit one is several times longer).
+__device__ __forceinline__ int64_t mul_div_floor(int64_t x, int64_t y, int64_t z) {
+  const uint64_t n = (uint64_t)x * (uint64_t)y;
+  if ((n >> 32) == 0 && ((uint64_t)z >> 32) == 0) return (int64_t)((uint32_t)n / (uint32_t)z);
+  return (int64_t)(n / (uint64_t)z);
+}
+
+// Units [u0, u1) of workgroup w under the cost split: u0 is the smallest unit
+// whose cost is at least floor(w * C / W) (U for w == W), and units[b0] <= u0.
+// Segment j = b * Hk + hk starts at cost units[b] + hk * G_b + P * j (G_b
+// groups per segment of sequence b), which grows with j. The last segment
+// starting at or below a cost T lies in the last sequence b whose first
+// segment does, cs(b) = units[b] + P * Hk * b <= T, at hk = min(Hk - 1,
+// (T - cs(b)) / (G_b + P)); the unit of cost T is T - P * j clamped to that
+// segment's units. Each wave finds b by counting the sequences with
+// cs(b) <= T, 64 per ballot (one LDS read per lane, no barrier), where a
+// binary search would chain ~2 log2(B Hk) dependent LDS reads and divisions
+// ahead of the workgroup's first page load.
+struct SplitRange {
+  int u0, u1, b0;
+};
+__device__ __forceinline__ SplitRange split_range(const int* units, int B, int Hk, int U, int W,
+                                                  int P, int w) {
   const int64_t C = (int64_t)U + (int64_t)P * B * Hk;
-  const int64_t T = (int64_t)w * C / W;
-  if (T >= C) return U;
-  if (P == 0) return (int)T;
-  // last segment j with cost(start of j) <= T
-  int lo = 0, hi = B * Hk - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    const int b = mid / Hk, hk = mid - b * Hk;
-    const int G = (units[b + 1] - units[b]) / Hk;
-    const int64_t start = (int64_t)units[b] + (int64_t)hk * G;
-    if (start + (int64_t)P * mid <= T) lo = mid; else hi = mid - 1;
+  const int64_t T0 = mul_div_floor(w, C, W);
+  const int64_t T1 = mul_div_floor(w + 1, C, W);
+  const int lane = threadIdx.x & 63;
+  int n0 = 0, n1 = 0;  // sequences b >= 1 with cs(b) <= T0, T1
+  for (int base = 1; base < B; base += 64) {
+    const int b = base + lane;
+    const int64_t cs = b < B ? (int64_t)units[b] + (int64_t)P * Hk * b : C + 1;
+    const uint64_t m1 = __ballot(cs <= T1);
+    n0 += __popcll(__ballot(cs <= T0));
+    n1 += __popcll(m1);
+    if (m1 != ~0ull) break;  // cs grows with b: no later sequence qualifies
   }
-  const int b = lo / Hk, hk = lo - b * Hk;
-  const int G = (units[b + 1] - units[b]) / Hk;
-  const int64_t start = (int64_t)units[b] + (int64_t)hk * G;
-  const int64_t u = T - (int64_t)P * lo;
-  return (int)min(max(u, start), start + G);
+  auto unit_at = [&](int64_t T, int b) -> int {
+    if (T >= C) return U;
+    if (P == 0) return (int)T;
+    const int64_t cs = (int64_t)units[b] + (int64_t)P * Hk * b;
+    const int G = (units[b + 1] - units[b]) / Hk;
+    const int hk = (int)min((int64_t)Hk - 1, mul_div_floor(T - cs, 1, G + P));
+    const int64_t start = (int64_t)units[b] + (int64_t)hk * G;
+    const int64_t u = T - (int64_t)P * ((int64_t)b * Hk + hk);
+    return (int)min(max(u, start), start + G);
+  };
+  SplitRange r;
+  r.u0 = unit_at(T0, n0);
+  r.u1 = unit_at(T1, n1);
+  r.b0 = n0;
+  return r;
 }
 
 // Balanced decode. The work is the list of units (sequence b, KV head hk,
@@ -330,8 +361,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     for (int b = tid; b <= p.B; b += kDecodeThreads) p.ws_units[b] = s_units[b];
   }
   const int P = split_cost_p(p, U, W);
-  const int u0 = split_start(s_units, p.B, p.Hk, U, W, P, w);
-  const int u1 = split_start(s_units, p.B, p.Hk, U, W, P, w + 1);
+  const SplitRange range = split_range(s_units, p.B, p.Hk, U, W, P, w);
+  // The range is wave-uniform; the LDS reads it comes from leave it in VGPRs,
+  // and the buffer resources built from it would then be rebuilt per lane
+  // (a readfirstlane loop around every K/V load).
+  const int u0 = __builtin_amdgcn_readfirstlane(range.u0);
+  const int u1 = __builtin_amdgcn_readfirstlane(range.u1);
   if (u0 >= u1) return;
 
   const f16* qp = reinterpret_cast<const f16*>(p.q);
@@ -626,13 +661,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 
   };
 
-  // First sequence with units at u0, then the segments of [u0, u1).
-  int lo = 0, hi = p.B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (s_units[mid] <= u0) lo = mid; else hi = mid - 1;
-  }
-  int b = lo;
+  // The segments of [u0, u1), from the sequence the split found.
+  int b = __builtin_amdgcn_readfirstlane(range.b0);
   for (int u = u0; u < u1;) {
     while (s_units[b + 1] <= u) ++b;
     const int G = (s_units[b + 1] - s_units[b]) / p.Hk;
