@@ -42,6 +42,8 @@ sys.path.insert(0, REPO)
 
 from hrm_flashrenderer_amd import (build_rope_cache, flash_attn, flash_attn_paged,  # noqa: E402
                                    paged_kv_append, workloads)
+from hrm_flashrenderer_amd import _lib  # noqa: E402
+from hrm_flashrenderer_amd.ops import heads_per_kv  # noqa: E402
 from hrm_flashrenderer_amd.token_major import decode_token_major  # noqa: E402
 from hrm_flashrenderer_amd.token_major import workspace_bytes as token_major_workspace  # noqa: E402
 
@@ -245,10 +247,12 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
 
 def bench_decode_rows(w, steps, warmup, rows=(1, 4, 8, 16)):
     """Paged attention over cfg4's pool with M query rows per sequence (the
-    last M positions, causal: speculative or short-chunk decode). M = 1, 4
-    and 8 take the decode kernels (M * 64/8 heads <= 64); M = 16 (128 rows per
-    KV head) takes the prefill kernel with 16 of its 128 rows live per q head.
-    GB/s counts the live K/V, q/o, block table and seqlen bytes once."""
+    last M positions, causal: speculative or short-chunk decode). M = 1 and 4
+    take the decode kernels; M = 8 and 16 (64 and 128 rows per KV head over
+    64 sequences) take the prefill kernel's packed layout, which fills 128-row
+    tiles with the (head, position) rows of one KV head (the library picks the
+    path; `path` reports it). GB/s counts the live K/V, q/o, block table and
+    seqlen bytes once."""
     res = {}
     dev = w.q.device
     g = torch.Generator(device=dev)
@@ -264,9 +268,11 @@ def bench_decode_rows(w, steps, warmup, rows=(1, 4, 8, 16)):
                              block_table=w.block_table)
 
         _, mean_ms = back_to_back(step, steps, warmup)
+        ws = _lib.load().fa_paged_workspace_bytes(w.B, w.Hq, M, w.D, w.Hk, w.block_table.size(1),
+                                                  16, heads_per_kv(w.head_map, w.Hk))
         res[f"M{M}"] = {"kernel_ms_back_to_back": round(mean_ms, 4), "bytes_per_step": nbytes,
                         "roofline": roofline("hbm", nbytes, mean_ms),
-                        "path": "decode" if M * (w.Hq // w.Hk) <= 64 else "prefill"}
+                        "path": "decode" if ws > 0 else "prefill (packed rows)"}
     return res
 
 

@@ -165,6 +165,7 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
   p.M = M;
   p.N = N;
   p.group = Hq / Hk;
+  p.pack_heads = p.group;  // rows of one KV head's q heads share 128-row tiles when M < 128
   p.causal = causal ? 1 : 0;
   p.q_offset = narrow(q_offset);
   p.k_offset = narrow(k_offset);
@@ -176,7 +177,7 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacity_pages,
                                 int page_size, int heads_per_kv) {
   if (B <= 0 || Hq <= 0 || M <= 0 || Hk <= 0 || !head_dim_ok(D)) return 0;
-  if (!fa::use_decode_path(B, M, Hq, Hk)) return 0;
+  if (!fa::use_decode_path(B, M, Hq, Hk, heads_per_kv)) return 0;
   const int cap = capacity_tokens(capacity_pages < 0 ? 0 : capacity_pages,
                                   page_size < 1 ? 1 : page_size);
   return fa::plan_decode(B, Hq, M, D, Hk, cap, heads_per_kv).ws_bytes;
@@ -189,7 +190,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                      const int32_t* q_lens, const int32_t* block_table, int max_blocks,
                      int heads_per_kv, void* workspace,
                      size_t workspace_bytes, const void* rope_cos, const void* rope_sin,
-                     int rope_len, void* stream) {
+                     int rope_len, void* stream, bool decode_ok = true) {
   if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
   int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
   if (rc != FA_OK) return rc;
@@ -226,7 +227,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
   p.rope_len = rope_len;
 
   (void)hipGetLastError();
-  if (fa::use_decode_path(B, M, Hq, Hk)) {
+  if (decode_ok && fa::use_decode_path(B, M, Hq, Hk, heads_per_kv)) {
     const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N, heads_per_kv);
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
@@ -240,6 +241,9 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
     p.dec_rows = plan.rows;
     return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
   }
+  // the prefill kernel packs the rows of a KV head's q heads (at most
+  // heads_per_kv of them) into shared 128-row tiles when M < 128
+  p.pack_heads = heads_per_kv > 0 ? std::min(heads_per_kv, Hq) : 0;
   return launch_status(fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream));
 }
 
@@ -282,8 +286,13 @@ int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const vo
                                     const int32_t* block_table, int max_blocks,
                                     int heads_per_kv, void* stream) {
   const int cap_pages = block_table != nullptr ? max_blocks : P;
-  const size_t need =
-      fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size, heads_per_kv);
+  size_t need = fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size, heads_per_kv);
+  // More than 64 query rows per KV head also run on the prefill kernel, which
+  // needs no scratch: it takes them when the decode kernels' passes would not
+  // fit the scratch.
+  const bool rows_gt_64 = Hk > 0 && (int64_t)M * ((Hq + Hk - 1) / Hk) > 64;
+  const bool decode_ok = need <= kScratchBytes || !rows_gt_64;
+  if (!decode_ok) need = 0;
   if (need > kScratchBytes)
     return fail(FA_ERR_WORKSPACE,
                 "these shapes need %zu bytes of decode scratch; the allocation-free entry "
@@ -297,7 +306,7 @@ int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const vo
   return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
                    causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
                    max_blocks, heads_per_kv, ws, need > 0 ? kScratchBytes : 0, nullptr, nullptr,
-                   0, stream);
+                   0, stream, decode_ok);
 }
 
 static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,
@@ -366,7 +375,7 @@ static int token_major_hpk(int H, int KVH, int heads_per_kv, bool engine_map) {
 size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max,
                                              int heads_per_kv) {
   if (H <= 0 || KVH <= 0 || !head_dim_ok(Dh) || t_max < 0 || t_max >= INT_MAX) return 0;
-  if (!fa::use_decode_path(1, 1, H, KVH)) return 0;
+  if (!fa::use_decode_path(1, 1, H, KVH, 0)) return 0;
   const int hpk = token_major_hpk(H, KVH, heads_per_kv, false);
   return fa::plan_decode(1, H, 1, Dh, KVH, t_max + 1, hpk).ws_bytes;
 }
@@ -379,7 +388,7 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   if (!head_dim_ok(Dh)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
   if (t < 0 || t >= INT_MAX) return fail(FA_ERR_INVALID, "position t out of range");
   if (!isfinite(scale)) return fail(FA_ERR_INVALID, "scale must be finite");
-  if (!fa::use_decode_path(1, 1, H, KVH))
+  if (!fa::use_decode_path(1, 1, H, KVH, 0))
     return fail(FA_ERR_INVALID, "unsupported head counts H=%d KVH=%d", H, KVH);
   if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr)
     return fail(FA_ERR_INVALID, "null tensor pointer");

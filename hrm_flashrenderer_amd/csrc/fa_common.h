@@ -120,6 +120,10 @@ struct AttnParams {
   int q_f32;
   int o_f32;
   int head_mod;
+  // prefill with M < 128 rows per q head: > 0 packs the (head, position) rows
+  // of each KV head's q heads into 128-row tiles, at most pack_heads heads
+  // per KV head (fa_prefill.hip); 0 keeps one q head per tile
+  int pack_heads;
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
@@ -211,6 +215,10 @@ int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D);
 // with two decode workgroups per CU (a sweep of 0-32 peaks at 12-16 for both
 // benchmark decode shapes).
 constexpr int kSegmentCost = 12;
-bool use_decode_path(int B, int M, int Hq, int Hk);
+// Whether paged attention with M query rows per sequence runs on the decode
+// kernels (split over the device, partial results merged by a second
+// kernel; needs the workspace of plan_decode) or on the prefill kernel.
+constexpr int kPackedMinTiles = 256;
+bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv);
 
 }  // namespace fa

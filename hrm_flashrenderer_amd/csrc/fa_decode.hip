@@ -903,10 +903,26 @@ int decode_grid_wgs(int D, DecodeVariant var) {
 
 }  // namespace
 
-bool use_decode_path(int B, int M, int Hq, int Hk) {
-  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch) return false;
-  const int group = (Hq + Hk - 1) / Hk;
-  return M >= 1 && (int64_t)M * group <= 4 * kRows;
+bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv) {
+  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch || M < 1) return false;
+  const int64_t rows = (int64_t)M * ((Hq + Hk - 1) / Hk);  // query rows per KV head
+  if (rows <= 2 * kRows) return true;
+  // With M < 128 and a heads_per_kv bound, the prefill kernel packs a KV
+  // head's (head, position) rows into 128-row tiles: one pass over its pages
+  // for all of them at prefill MFMA rates. That wins once the tiles fill the
+  // device; with fewer, the decode kernels (split over the whole device)
+  // serve the rows in passes of up to 64. Over cfg4's pool at 64/8 heads,
+  // M = 16 (two decode passes): B = 1 82 us decode against 293 packed, B = 16
+  // 358 against 361, B = 32 (256 tiles) packed 396, B = 64 559 against 1281;
+  // M = 8 (one decode pass, half-empty tiles): B = 32 350 decode against 389
+  // packed, B = 64 (512 tiles) 512 packed against 651.
+  const bool packable = heads_per_kv >= 2 && M < 128;
+  if (packable) {
+    const int64_t hpk = std::min(heads_per_kv, Hq);
+    const int64_t tiles = (int64_t)B * Hk * ((hpk * M + 127) / 128);
+    if (tiles >= (rows <= 4 * kRows ? 2 : 1) * kPackedMinTiles) return false;
+  }
+  return rows <= 4 * kRows || (packable && rows <= 16 * kRows);
 }
 
 int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {

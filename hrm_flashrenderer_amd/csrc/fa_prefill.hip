@@ -39,6 +39,7 @@ namespace fa {
 namespace {
 
 constexpr int kBM = 128;     // query rows per workgroup
+constexpr int kMaxPackHeads = 256;  // q heads listed per KV head in the packed layout
 constexpr int kBN = 64;      // keys per tile
 constexpr int kThreads = 256;
 
@@ -606,7 +607,16 @@ __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* vo
 // workgroup (32 KB), at most 168 VGPRs, so three workgroups (three waves per
 // SIMD) share a CU, whose waves hide each other's latency.
 // ---------------------------------------------------------------------------
-template <int D>
+//
+// PACKED: the 128 rows of a workgroup are (head, position) rows of one KV
+// head instead of 128 positions of one q head. Row r of the (sequence, KV
+// head) pair's packed list is position r % M of the (r / M)-th q head that
+// reads the KV head (head-map order), so a pair's K/V streams once for all
+// its q heads when M < 128 (e.g. 16 positions x 8 heads in one tile, where
+// the per-head layout would fill 16 of 128 rows and stream the K/V once per
+// q head). `ntq` is then the number of 128-row tiles per pair, `group` 1,
+// and slot L runs pair L / ntq (consecutive pairs go to different XCDs).
+template <int D, bool PACKED>
 __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, int ntq,
                                                                   int group, int per_xcd,
                                                                   int total) {
@@ -617,21 +627,28 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
   __shared__ __attribute__((aligned(1024))) char smem[4 * TILE];  // K0 V0 K1 V1
+  // PACKED: the q heads of the pair's KV head in head-map order, and the
+  // heads whose head-map entry is outside [0, Hk) (collected by the pairs of
+  // KV head 0); s_pk_n holds both counts.
+  constexpr int kPackList = PACKED ? kMaxPackHeads : 1;
+  __shared__ int s_pk[kPackList];
+  __shared__ int s_bad[kPackList];
+  __shared__ int s_pk_n[2];
 
   const int slot = blockIdx.x;
-  const int item = (slot & 7) * per_xcd + (slot >> 3);
+  const int item = PACKED ? slot : (slot & 7) * per_xcd + (slot >> 3);
   if (item >= total) return;
   const int per_pair = ntq * group;
   int pair = item / per_pair;
   int rem = item - pair * per_pair;
   int qt = ntq - 1 - rem / group;
   int head = rem % group;
-  const int ngroups = p.Hq / group;
+  const int ngroups = PACKED ? p.Hk : p.Hq / group;
   // With `pre`, the sequence data of the chosen pair come from the loads that
   // ordered the pairs (kv_len_pre, hk_pre, qo_pre, ko_pre).
   bool pre = false;
   int kv_len_pre = 0, hk_pre = 0, qo_pre = 0, ko_pre = 0, qlen_pre = 0;
-  if (per_xcd % per_pair == 0 && total == 8 * per_xcd) {
+  if (!PACKED && per_xcd % per_pair == 0 && total == 8 * per_xcd) {
     // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
     // x + 8, x + 16, ..., so sequences of different lengths spread over all
     // XCDs.
@@ -694,8 +711,9 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     qt = ntq - 1 - r;
     head = w % group;
   }
-  const int hq = (pair % ngroups) * group + head;
   const int b = pair / ngroups;
+  const int hk_pair = pair % ngroups;  // PACKED: the pair's KV head
+  const int hq = PACKED ? 0 : hk_pair * group + head;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -703,7 +721,48 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const int col = lane & 31;
   const int half_id = lane >> 5;
   const int q0 = qt * kBM;
-  const int qrow = q0 + wave * 32 + col;
+  // PACKED: wave 0 lists the q heads of KV head hk_pair in head-map order (64
+  // heads per ballot); the pairs of KV head 0 also list the heads whose entry
+  // is outside [0, Hk).
+  int pk_count = 0, pk_rows = 0;
+  if constexpr (PACKED) {
+    if (wave == 0) {
+      int count = 0, nbad = 0;
+      for (int base = 0; base < p.Hq; base += 64) {
+        const int h = base + lane;
+        const int hm = h < p.Hq ? p.kv_head(h) : -2;
+        const bool match = hm == hk_pair;
+        const bool bad = hk_pair == 0 && hm == -1;
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint64_t mm = __ballot(match), mb = __ballot(bad);
+        if (match) {
+          const int pos = count + __popcll(mm & below);
+          if (pos < kMaxPackHeads) s_pk[pos] = h;
+        }
+        if (bad) {
+          const int pos = nbad + __popcll(mb & below);
+          if (pos < kMaxPackHeads) s_bad[pos] = h;
+        }
+        count += __popcll(mm);
+        nbad += __popcll(mb);
+      }
+      if (lane == 0) {
+        s_pk_n[0] = min(count, kMaxPackHeads);
+        s_pk_n[1] = min(nbad, kMaxPackHeads);
+      }
+    }
+    __syncthreads();
+    // Heads past pack_heads (a head map that sends more heads to one KV head
+    // than the caller stated) get no packed rows: tile 0 writes them as NaN.
+    pk_count = min(s_pk_n[0], p.pack_heads);
+    pk_rows = pk_count * p.M;
+  }
+  // This lane's query row: position qrow of q head hq_row.
+  const int prow = q0 + wave * 32 + col;  // PACKED: row of the pair's packed list
+  const int pj = PACKED ? prow / p.M : 0;
+  const bool row_exists = PACKED ? prow < pk_rows : true;
+  const int qrow = PACKED ? prow - pj * p.M : prow;
+  const int hq_row = PACKED ? (row_exists ? s_pk[pj] : 0) : hq;
   f16* op = reinterpret_cast<f16*>(p.o) + ((int64_t)b * p.Hq + hq) * p.M * D;
 
   // The loads that need only (b, hq) leave first, together with the scalar
@@ -712,18 +771,19 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // tiles. No branch separates them from their uses, so the compiler keeps
   // them here; a head-map entry outside [0, Hk) runs no tiles and writes NaN
   // rows through the common epilogue.
-  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq) * p.M * D;
+  const f16* qp = reinterpret_cast<const f16*>(p.q) + ((int64_t)b * p.Hq + hq_row) * p.M * D;
   const int64_t qoff = (int64_t)min(qrow, p.M - 1) * D + 8 * half_id;
+  const bool q_ok = qrow < p.M && row_exists;
   half8 qreg[KSTEPS];
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
     const half8 v = *reinterpret_cast<const half8*>(qp + qoff + 16 * ks);
-    qreg[ks] = qrow < p.M ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    qreg[ks] = q_ok ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   using Table = SlabTable<D, NW, BN>;
   const typename Table::RowReq req0 = Table::row_load(p, b, lane, wave);
   const SeqData sd = seq_data(p, b, hq);
-  const int hk = pre ? hk_pre : sd.hk;
+  const int hk = PACKED ? hk_pair : pre ? hk_pre : sd.hk;
   const int kv_len = pre ? kv_len_pre : sd.kv_len;
   const int qo = pre ? qo_pre : sd.qo;
   const int ko = pre ? ko_pre : sd.ko;
@@ -734,14 +794,40 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   pages.rows = Table::row_finish(p, b, req0);
   pages.hk_rows = head_ok ? (uint32_t)((int64_t)hk * (p.kv.stride_hk / D)) : 0u;
 
-  const int last_row = min(q0 + kBM, qlen) - 1;
-  const int wg_lim = head_ok && q0 < qlen ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
+  int wg_lim, wave_lim_max, wave_lim_min;
+  if constexpr (PACKED) {
+    // First and last position held by packed rows [r0, r1) that are not
+    // padding (position < qlen), when there is such a row.
+    auto positions = [&](int r0, int r1, int& pmin, int& pmax) {
+      r1 = min(r1, pk_rows);
+      if (r1 <= r0) return false;
+      if (r1 - r0 >= p.M) {
+        pmin = 0;
+        pmax = p.M - 1;
+      } else {
+        const int s0 = r0 % p.M, s1 = (r1 - 1) % p.M;
+        pmin = s0 <= s1 ? s0 : 0;
+        pmax = s0 <= s1 ? s1 : p.M - 1;
+      }
+      if (pmin >= qlen) return false;
+      pmax = min(pmax, qlen - 1);
+      return true;
+    };
+    int pmin = 0, pmax = 0;
+    wg_lim = positions(q0, q0 + kBM, pmin, pmax) ? row_key_limit(kv_len, p.causal, qo, ko, pmax) : 0;
+    const bool any = positions(q0 + wave * 32, q0 + wave * 32 + 32, pmin, pmax);
+    wave_lim_max = any ? row_key_limit(kv_len, p.causal, qo, ko, pmax) : 0;
+    wave_lim_min = any ? row_key_limit(kv_len, p.causal, qo, ko, pmin) : 0;
+  } else {
+    const int last_row = min(q0 + kBM, qlen) - 1;
+    wg_lim = head_ok && q0 < qlen ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
+    const int wrow0 = q0 + wave * 32;
+    const int wrow1 = min(wrow0 + 31, qlen - 1);
+    const bool wave_rows = wrow0 < qlen;
+    wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
+    wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
+  }
   const int ntiles = (wg_lim + BN - 1) / BN;
-  const int wrow0 = q0 + wave * 32;
-  const int wrow1 = min(wrow0 + 31, qlen - 1);
-  const bool wave_rows = wrow0 < qlen;
-  const int wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
-  const int wave_lim_min = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow0) : 0;
   const int lim = row_key_limit(kv_len, p.causal, qo, ko, qrow);
 
   const char* kp = reinterpret_cast<const char*>(p.k);
@@ -754,7 +840,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   }
   QuarterSrc next_src = pages.get(p, b, 1, kv_len, wave, lane);
 
-  if (p.rope_cos != nullptr && qrow < p.M) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
+  if (p.rope_cos != nullptr && q_ok) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
   // LDS byte offsets of the lane's operands. K: row col, logical chunk
   // 2*ks + half_id at chunk ^ swz_k(col); the chunk bits of 2*ks and half_id
@@ -891,7 +977,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   // half of 16-byte chunk 4i + g.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = !head_ok ? __builtin_nanf("") : kv_len == 0 ? 0.f : 1.f / l_tot;
-  const bool live = qrow < qlen;  // padding rows are zeros whatever their Q held
+  const bool live = qrow < qlen && row_exists;  // padding rows are zeros whatever their Q held
   __syncthreads();  // every wave has finished reading the last K/V stage
   const int lrow = wave * 32 + col;
 #pragma unroll
@@ -906,14 +992,41 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     }
   }
   __syncthreads();
-  const int rows = min(kBM, p.M - q0);
+  const int rows = min(kBM, (PACKED ? pk_rows : p.M) - q0);
   f16* ob = op + (int64_t)q0 * D;
   for (int e = tid; e < rows * C::CH; e += kThreads) {
     const int r = e / C::CH, ch = e % C::CH;
     const half8 v = *reinterpret_cast<const half8*>(smem + r * C::ROWB + 16 * (ch ^ C::swz_k(r)));
+    f16* dst;
+    if constexpr (PACKED) {
+      const int pr = q0 + r, j = pr / p.M;
+      dst = reinterpret_cast<f16*>(p.o) + (((int64_t)b * p.Hq + s_pk[j]) * p.M + (pr - j * p.M)) * D;
+    } else {
+      dst = ob + (int64_t)r * D;
+    }
     // O is not read again by this kernel: a non-temporal store keeps the
     // K/V lines that other workgroups still read in L2.
-    __builtin_nontemporal_store(v, reinterpret_cast<half8*>(ob + (int64_t)r * D + 8 * ch));
+    __builtin_nontemporal_store(v, reinterpret_cast<half8*>(dst + 8 * ch));
+  }
+  if constexpr (PACKED) {
+    // Tile 0 of each pair writes the rows no packed row covers: the pair's
+    // heads past pack_heads and, for KV head 0, the heads whose head-map
+    // entry is outside [0, Hk): NaN, padding positions zero, as the
+    // per-head layout writes them.
+    if (qt == 0) {
+      const int extra = max(s_pk_n[0] - pk_count, 0);
+      const int nh = extra + s_pk_n[1];
+      const f16 qnan = (f16)__builtin_nanf("");
+      const half8 nan8 = half8{qnan, qnan, qnan, qnan, qnan, qnan, qnan, qnan};
+      for (int e = tid; e < nh * p.M * C::CH; e += kThreads) {
+        const int ch = e % C::CH, rowi = e / C::CH;
+        const int i = rowi / p.M, pos = rowi - i * p.M;
+        const int h = i < extra ? s_pk[pk_count + i] : s_bad[i - extra];
+        const half8 v = pos < qlen ? nan8 : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        f16* d = reinterpret_cast<f16*>(p.o) + (((int64_t)b * p.Hq + h) * p.M + pos) * D;
+        *reinterpret_cast<half8*>(d + 8 * ch) = v;
+      }
+    }
   }
 }
 
@@ -1072,6 +1185,15 @@ __global__ __launch_bounds__(64 * kF32Waves) void prefill_f32_kernel(AttnParams 
 
 }  // namespace
 
+// The packed layout serves calls with fewer than 128 rows per q head and at
+// least two q heads per KV head (pack_heads, from the caller's heads_per_kv),
+// on the tile-DMA kernel: it fills 128-row tiles with the (head, position)
+// rows of a KV head, where one q head per tile would leave rows empty and
+// stream the KV head's pages once per q head.
+static bool use_packed_rows(const AttnParams& p) {
+  return p.pack_heads >= 2 && p.M < kBM && p.Hq <= kMaxPackHeads && p.Hk > 0;
+}
+
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream) {
   if (dtype == 1) {
     const dim3 grid((unsigned)((p.M + kF32Rows - 1) / kF32Rows), (unsigned)p.Hq, (unsigned)p.B);
@@ -1091,16 +1213,29 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
       hipLaunchKernelGGL((prefill_f16_kernel<64, false>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
   }
+  if (use_packed_rows(p)) {
+    // (head, position) rows of each KV head packed into 128-row tiles
+    const int ntp = (int)(((int64_t)p.pack_heads * p.M + kBM - 1) / kBM);
+    const int total = ntp * p.Hk * p.B;
+    const dim3 grid((unsigned)total);
+    if (D == 128)
+      hipLaunchKernelGGL((prefill_b32_kernel<128, true>), grid, dim3(kThreads), 0, stream, p, ntp, 1,
+                         0, total);
+    else
+      hipLaunchKernelGGL((prefill_b32_kernel<64, true>), grid, dim3(kThreads), 0, stream, p, ntp, 1,
+                         0, total);
+    return hipGetLastError();
+  }
   const int group = (p.Hk > 0 && p.Hq % p.Hk == 0) ? p.Hq / p.Hk : 1;
   const int total = ntq * p.Hq * p.B;
   const int per_xcd = (total + 7) / 8;
   const dim3 grid((unsigned)(8 * per_xcd));
   if (D == 128)
-    hipLaunchKernelGGL(prefill_b32_kernel<128>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                       per_xcd, total);
+    hipLaunchKernelGGL((prefill_b32_kernel<128, false>), grid, dim3(kThreads), 0, stream, p, ntq,
+                       group, per_xcd, total);
   else
-    hipLaunchKernelGGL(prefill_b32_kernel<64>, grid, dim3(kThreads), 0, stream, p, ntq, group,
-                       per_xcd, total);
+    hipLaunchKernelGGL((prefill_b32_kernel<64, false>), grid, dim3(kThreads), 0, stream, p, ntq,
+                       group, per_xcd, total);
   return hipGetLastError();
 }
 

@@ -91,10 +91,13 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
  *   heads_per_kv : the most query heads head_map sends to one KV head
  *              (Hq/Hk for the usual GQA map hq // (Hq/Hk)); <= 0 means Hq,
  *              no assumption. It sizes the decode workspace, whose partial
- *              slots each hold one KV head's query rows. If head_map sends
+ *              slots each hold one KV head's query rows, and, with M < 128
+ *              off the decode path, lets the prefill kernel pack the
+ *              (head, position) rows of a KV head's q heads into shared
+ *              128-row tiles (one pass over the KV head's pages for all of
+ *              them; <= 0 keeps one q head per tile). If head_map sends
  *              more heads to a KV head, the heads past the bound get NaN rows
- *              on the decode path (M * ceil(Hq/Hk) <= 64); nothing is written
- *              out of bounds.
+ *              on both paths; nothing is written out of bounds.
  *   workspace : device scratch of at least fa_paged_workspace_bytes(...)
  *               bytes for the same arguments (may be NULL when that is 0);
  *               its contents need no initialisation.
@@ -118,9 +121,12 @@ int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pa
  * launcher allocates its output with torch (csrc/flash_attn_sm75.cu:492).
  * It allocates nothing: the decode path's partial results go to a static
  * device array of 32 MiB per GPU, held until the process ends. Arguments and
- * results are those of fa_flash_attn_paged_fwd; shapes whose decode
- * workspace (fa_paged_workspace_bytes) exceeds 32 MiB are rejected with
- * FA_ERR_WORKSPACE before anything is launched. All calls on one GPU share
+ * results are those of fa_flash_attn_paged_fwd, except that shapes with more
+ * than 64 query rows per KV head (M * ceil(Hq/Hk)) whose decode workspace
+ * (fa_paged_workspace_bytes) exceeds 32 MiB run on the prefill kernel, which
+ * needs none (same results within the fp32-softmax tolerance, not bit for
+ * bit); other shapes beyond 32 MiB are rejected with FA_ERR_WORKSPACE before
+ * anything is launched. All calls on one GPU share
  * its scratch, so calls that overlap on one GPU (concurrent streams, or
  * threads without ordering) race; calls ordered on one stream do not. The
  * scratch needs no initialisation and keeps the last call's contents.

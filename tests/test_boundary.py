@@ -141,6 +141,18 @@ def test_workspace_sizing_depends_on_sizes_only():
     # prefill-shaped calls need no workspace
     assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16, 5) == 0
     assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16, 1) == 0
+    # More than 32 query rows per KV head (M * ceil(Hq/Hk)) with a
+    # heads_per_kv bound: the packed prefill layout (no workspace) once the
+    # batch gives 256 tiles of 128 rows (512 while one 64-row decode pass
+    # would do), below that the decode kernels in passes of up to 64 rows (at
+    # most 256 rows); without a bound, one decode pass or the per-head
+    # prefill layout.
+    for B, M, hpk, decode in ((64, 16, 8, False), (32, 16, 8, False), (16, 16, 8, True),
+                              (2, 32, 8, True), (2, 33, 8, False), (64, 8, 8, False),
+                              (32, 8, 8, True), (64, 4, 8, True), (2, 16, 0, False),
+                              (64, 8, 0, True)):
+        ws = lib.fa_paged_workspace_bytes(B, 64, M, 128, 8, 1025, 16, hpk)
+        assert (ws > 0) == decode, (B, M, hpk)
     # token-major decode: one sequence of t_max + 1 keys, rows = heads per KV head
     t_max = 4095  # 256 groups x 8 KV heads = 2048 units -> 256 workgroups
     slots = 8 + 256

@@ -360,12 +360,16 @@ def test_decode_few_rows(gpu, M, causal):
     (64, 8, 8, 128, True, 24),    # per-row loads (page size 24): two passes of two blocks
     (32, 4, 8, 64, True, 16),     # 64 rows at D=64: four blocks in one pass
     (16, 4, 12, 64, False, 16),   # 48 rows: three live blocks of four
+    (64, 8, 16, 128, True, 16),   # 128 rows, few sequences: two passes of four blocks
+    (64, 8, 32, 128, True, 16),   # 256 rows: four passes
+    (40, 8, 30, 64, True, 16),    # 150 rows at D=64: three passes, the last part-filled
 ])
 def test_decode_row_blocks_per_pass(gpu, Hq, Hk, M, D, causal, ps):
     """The decode kernels serve up to 4 blocks of 16 query rows per pass over a
-    KV head's pages (2 with per-row loads at D=128, which walk larger groups in
-    passes); every head of every sequence is checked, with ragged lengths (one
-    empty) and NaN-poisoned dead slots."""
+    KV head's pages (2 with per-row loads at D=128) and walk larger groups in
+    passes (up to 256 rows per KV head when the batch is too small for the
+    packed prefill layout); every head of every sequence is checked, with
+    ragged lengths (one empty) and NaN-poisoned dead slots."""
     lengths = [700, 0, 1500, 33, 2100]
     c = _small_paged(5, Hq, Hk, M, lengths, PS=ps, D=D, seed=330 + M + D, causal=causal,
                      q_offsets=[max(0, n - M) for n in lengths] if causal else None)

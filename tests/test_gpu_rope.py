@@ -55,10 +55,11 @@ def test_append_rope_bitexact(gpu, D):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("M,causal", [(1, False), (3, True), (150, True)])
+@pytest.mark.parametrize("M,causal", [(1, False), (3, True), (40, True), (150, True)])
 def test_attention_with_rotary_queries(gpu, D, M, causal):
     """Cache appends with rotated keys, attention rotating q in the kernel,
-    against fp64 attention over the oracle's rotated q and k."""
+    against fp64 attention over the oracle's rotated q and k (M = 40: the
+    packed-row prefill layout, 160 rows per KV head)."""
     B, Hq, Hk, PS = 2, 8, 2, 16
     L = 2048
     cos, sin = _tables(L, D, gpu)

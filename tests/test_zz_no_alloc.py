@@ -3,8 +3,9 @@ through the C ABI: its outputs must equal fa_flash_attn_paged_fwd's (same
 kernels; the decode partials live in the library's static scratch instead of
 a caller workspace) on two calls in a row, the second smaller than the first
 (the scratch keeps the first call's contents), on a prefill call (no
-scratch), and with a per-call stream; shapes whose workspace exceeds the
-scratch are rejected before any launch."""
+scratch), and with a per-call stream; more than 64 rows per KV head beyond
+the scratch run on the prefill kernel, other shapes whose workspace exceeds
+the scratch are rejected before any launch."""
 import ctypes
 
 import pytest
@@ -81,12 +82,25 @@ def test_no_alloc_entry_matches_the_workspace_entry(gpu):
         assert torch.isfinite(new).all(), name
 
 
+def test_no_alloc_entry_runs_many_rows_on_the_prefill_kernel(gpu):
+    """256 query rows per KV head over two sequences: the workspace entry runs
+    the decode kernels in four passes (its workspace is beyond the 32 MiB
+    scratch); the allocation-free entry takes the prefill kernel instead, with
+    the same results within the fp32-softmax tolerance."""
+    from paged_ref import assert_close
+    c = _case(2, 64, 8, 32, [3000, 777], 950, True)
+    ref, new, ws_bytes = _both(c)
+    assert ws_bytes > 32 << 20
+    assert torch.isfinite(new).all()
+    assert_close(new.numpy(), ref.double().numpy(), "no-alloc prefill vs decode passes")
+
+
 def test_no_alloc_entry_rejects_shapes_beyond_its_scratch(gpu):
     lib = _lib.load()
     P = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
-    need = lib.fa_paged_workspace_bytes(2048, 64, 8, 128, 8, 2049, 16, 8)
+    need = lib.fa_paged_workspace_bytes(2048, 64, 1, 128, 8, 2049, 16, 8)
     assert need > 32 << 20
-    rc = lib.fa_flash_attn_paged_fwd_noalloc(P, P, P, P, 16, P, P, 2048, 64, 8, 128, 1, 8, 40000,
+    rc = lib.fa_flash_attn_paged_fwd_noalloc(P, P, P, P, 16, P, P, 2048, 64, 1, 128, 1, 8, 40000,
                                               0, 0, 0, None, None, None, P, 2049, 8, None)
     msg = lib.fa_last_error().decode()
     assert rc == -3 and "allocation-free entry holds 33554432" in msg, msg
