@@ -41,7 +41,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 from hrm_flashrenderer_amd import (build_rope_cache, flash_attn, flash_attn_paged,  # noqa: E402
-                                   paged_kv_append, workloads)
+                                   flash_attn_paged_append, paged_kv_append, workloads)
 from hrm_flashrenderer_amd import _lib  # noqa: E402
 from hrm_flashrenderer_amd.ops import heads_per_kv  # noqa: E402
 from hrm_flashrenderer_amd.token_major import decode_token_major  # noqa: E402
@@ -243,6 +243,41 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
         out["append_bytes_per_step"] = abytes
         out["end_to_end_ms"] = round(mean_step, 4)
     return out
+
+
+def bench_decode_fused(w, steps, warmup, two_call, rope=None):
+    """cfg4's step (append one token per sequence, then decode) as one call,
+    flash_attn_paged_append: the decode kernel takes the new token from
+    k_new / v_new and the merge kernel writes it into the pages, so the
+    append has no launch of its own. `two_call` is bench_decode's result for
+    the same workload (append kernel, then decode). GB/s counts the decode
+    bytes and the append's bytes over the fused step."""
+    nbytes = workloads.decode_bytes(w) + workloads.append_bytes(w)
+    stream = torch.cuda.current_stream()
+
+    def step(ev):
+        if ev:
+            ev[0].record(stream)
+        flash_attn_paged_append(w.q, w.k_pool, w.v_pool, w.k_new, w.v_new, w.seqlen, 16,
+                                w.head_map, False, w.append_pos if rope is not None else 0,
+                                start_pos=w.append_pos, block_table=w.block_table, rope=rope)
+        if ev:
+            ev[1].record(stream)
+
+    wall, mean_ms = back_to_back(step, steps, warmup)
+    _, segs = timed(step, steps, 0)
+    dec_ms = two_call["decode_kernel_ms_back_to_back"]
+    return {
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "step_ms_back_to_back": round(mean_ms, 4),
+        "step_ms": dist([x[0] for x in segs]),
+        "bytes_per_step": nbytes,
+        "roofline": roofline("hbm", nbytes, mean_ms),
+        "two_call_step_ms_back_to_back": two_call["end_to_end_ms"],
+        "decode_only_ms_back_to_back": dec_ms,
+        "append_cost_us": round((mean_ms - dec_ms) * 1e3, 2),
+        "append_cost_us_two_call": round((two_call["end_to_end_ms"] - dec_ms) * 1e3, 2),
+    }
 
 
 def bench_decode_rows(w, steps, warmup, rows=(1, 4, 8, 16)):
@@ -505,6 +540,11 @@ def main():
         extra["decode_cfg4_rope"] = bench_decode(w4, K, W, "decode_cfg4", traffic, rope=rope)
         log(f"cfg4 with fused rotary embedding: decode "
             f"{extra['decode_cfg4_rope']['roofline']['achieved']} GB/s")
+        extra["decode_cfg4_fused_append"] = bench_decode_fused(w4, K, W, extra["decode_cfg4"])
+        log(f"cfg4 fused append + decode: {extra['decode_cfg4_fused_append']['step_ms_back_to_back']}"
+            f" ms per step against {extra['decode_cfg4']['end_to_end_ms']} ms as two calls")
+        extra["decode_cfg4_fused_append_rope"] = bench_decode_fused(
+            w4, K, W, extra["decode_cfg4_rope"], rope=rope)
         extra["decode_cfg4_query_rows"] = bench_decode_rows(w4, K, W)
         log("cfg4 pool with M query rows: " + ", ".join(
             f"{k} {v['roofline']['achieved']} GB/s ({v['path']})"

@@ -14,7 +14,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 from ._build import LIB_PATH
 
-FA_ABI_VERSION = 2
+FA_ABI_VERSION = 3
 FA_DTYPE_F16 = 0
 FA_DTYPE_F32 = 1
 
@@ -42,6 +42,9 @@ SYMBOLS = (
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P, _P, _I, _P]),
     ("fa_paged_kv_scatter", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P]),
+    ("fa_flash_attn_paged_append_fwd", _I,
+     [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _I, _P, _P, _I,
+      _I64, _P, _P, _P, _I, _P, _SZ, _P]),
     ("fa_decode_token_major", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _I, _P, _SZ, _P]),
     ("fa_decode_token_major_workspace_bytes", _SZ, [_I, _I, _I, _I, _I]),

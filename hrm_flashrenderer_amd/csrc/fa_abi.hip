@@ -183,6 +183,16 @@ size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk, int capacit
   return fa::plan_decode(B, Hq, M, D, Hk, cap, heads_per_kv).ws_bytes;
 }
 
+// The new token of fa_flash_attn_paged_append_fwd (k_new / v_new
+// [B, Hk, 1, D]) and where it goes.
+struct AppendArgs {
+  const void* k_new;
+  const void* v_new;
+  int advance;                     // position seqlen[b]; seqlen[b] += 1 afterwards
+  int64_t start_pos;               // position without advance, unless start_positions
+  const int32_t* start_positions;  // nullable [B]
+};
+
 static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                      const int32_t* seqlen, int page_size, const int32_t* head_map, void* o, int B,
                      int Hq, int M, int D, int NB, int Hk, int P, int causal, int64_t q_offset,
@@ -190,14 +200,20 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                      const int32_t* q_lens, const int32_t* block_table, int max_blocks,
                      int heads_per_kv, void* workspace,
                      size_t workspace_bytes, const void* rope_cos, const void* rope_sin,
-                     int rope_len, void* stream, bool decode_ok = true) {
+                     int rope_len, void* stream, bool decode_ok = true,
+                     const AppendArgs* app = nullptr) {
   if (B < 0 || Hq < 0 || M < 0 || D < 0) return fail(FA_ERR_INVALID, "q [B,Hq,M,D]");
   int rc = check_pool(B, NB, Hk, P, page_size, block_table, max_blocks);
   if (rc != FA_OK) return rc;
   if (!head_dim_ok(D)) return fail(FA_ERR_INVALID, "Supported head_dim: 64 or 128");
-  if ((int64_t)B * Hq * M == 0) return FA_OK;
-  if (q == nullptr || o == nullptr || seqlen == nullptr || head_map == nullptr ||
-      ((int64_t)NB * P > 0 && (k_pages == nullptr || v_pages == nullptr)))
+  if (app != nullptr && (int64_t)B * Hk > 0 &&
+      (app->k_new == nullptr || app->v_new == nullptr || seqlen == nullptr ||
+       k_pages == nullptr || v_pages == nullptr))
+    return fail(FA_ERR_INVALID, "null tensor pointer");
+  if (app == nullptr && (int64_t)B * Hq * M == 0) return FA_OK;
+  if ((int64_t)B * Hq * M > 0 &&
+      (q == nullptr || o == nullptr || seqlen == nullptr || head_map == nullptr ||
+       ((int64_t)NB * P > 0 && (k_pages == nullptr || v_pages == nullptr))))
     return fail(FA_ERR_INVALID, "null tensor pointer");
 
   const int PS = page_size;
@@ -227,7 +243,37 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
   p.rope_len = rope_len;
 
   (void)hipGetLastError();
-  if (decode_ok && fa::use_decode_path(B, M, Hq, Hk, heads_per_kv)) {
+  const bool decode = decode_ok && fa::use_decode_path(B, M, Hq, Hk, heads_per_kv);
+  if (app != nullptr) {
+    p.app_advance = app->advance ? 1 : 0;
+    if (decode && rope_cos == nullptr && fa::fused_append_ok(B, M, Hq, Hk, heads_per_kv)) {
+      // the decode kernels take the new token (fa_decode.hip, APPEND)
+      p.app_k = reinterpret_cast<const fa::f16*>(app->k_new);
+      p.app_v = reinterpret_cast<const fa::f16*>(app->v_new);
+      p.app_positions = app->start_positions;
+      p.app_pos = narrow(app->start_pos);
+    } else {
+      // append kernel first (positions seqlen[b] with advance, read before
+      // the advance below), then the attention over the appended pages
+      hipError_t e = fa::launch_paged_append(
+          const_cast<void*>(k_pages), const_cast<void*>(v_pages), app->k_new, app->v_new, p.kv,
+          B, Hk, 1, narrow(app->start_pos), app->advance ? seqlen : app->start_positions,
+          nullptr, p.rope_cos, p.rope_sin, rope_len, (hipStream_t)stream);
+      if (e != hipSuccess) return launch_status(e);
+    }
+  }
+  hipError_t e = hipSuccess;
+  if ((int64_t)B * Hq * M == 0) {
+    // nothing to attend: the append alone
+    if (p.app_k != nullptr) {
+      p.app_k = nullptr;
+      e = fa::launch_paged_append(const_cast<void*>(k_pages), const_cast<void*>(v_pages),
+                                  app->k_new, app->v_new, p.kv, B, Hk, 1,
+                                  narrow(app->start_pos),
+                                  app->advance ? seqlen : app->start_positions, nullptr,
+                                  p.rope_cos, p.rope_sin, rope_len, (hipStream_t)stream);
+    }
+  } else if (decode) {
     const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N, heads_per_kv);
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
@@ -236,15 +282,20 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
     p.ws_o = reinterpret_cast<float*>(ws);
     p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
     p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
+    p.ws_app = p.ws_units + (B + 1);
     p.dec_wgs = fa::decode_launch_wgs(plan, p, D);
     p.dec_seg_cost = PS % 16 == 0 ? fa::kSegmentCost : 0;
     p.dec_rows = plan.rows;
-    return launch_status(fa::launch_decode(p, D, (hipStream_t)stream));
+    e = fa::launch_decode(p, D, (hipStream_t)stream);
+  } else {
+    // the prefill kernel packs the rows of a KV head's q heads (at most
+    // heads_per_kv of them) into shared 128-row tiles when M < 128
+    p.pack_heads = heads_per_kv > 0 ? std::min(heads_per_kv, Hq) : 0;
+    e = fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream);
   }
-  // the prefill kernel packs the rows of a KV head's q heads (at most
-  // heads_per_kv of them) into shared 128-row tiles when M < 128
-  p.pack_heads = heads_per_kv > 0 ? std::min(heads_per_kv, Hq) : 0;
-  return launch_status(fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream));
+  if (e == hipSuccess && app != nullptr && app->advance && p.app_k == nullptr)
+    e = fa::launch_advance_lengths(const_cast<int32_t*>(seqlen), B, (hipStream_t)stream);
+  return launch_status(e);
 }
 
 int fa_flash_attn_paged_fwd(const void* q, const void* k_pages, const void* v_pages,
@@ -307,6 +358,27 @@ int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const vo
                    causal, q_offset, k_offset, q_offsets, k_offsets, q_lens, block_table,
                    max_blocks, heads_per_kv, ws, need > 0 ? kScratchBytes : 0, nullptr, nullptr,
                    0, stream, decode_ok);
+}
+
+int fa_flash_attn_paged_append_fwd(const void* q, void* k_pages, void* v_pages, int32_t* seqlen,
+                                   int page_size, const int32_t* head_map, void* o, int B, int Hq,
+                                   int M, int D, int NB, int Hk, int P, int causal,
+                                   int64_t q_offset, const int32_t* q_offsets,
+                                   const int32_t* block_table, int max_blocks, int heads_per_kv,
+                                   const void* k_new, const void* v_new, int advance,
+                                   int64_t start_pos, const int32_t* start_positions,
+                                   const void* rope_cos, const void* rope_sin, int rope_len,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (advance != 0 && advance != 1) return fail(FA_ERR_INVALID, "advance must be 0 or 1");
+  if (advance && (start_positions != nullptr || start_pos != 0))
+    return fail(FA_ERR_INVALID, "with advance the positions are the lengths: no start positions");
+  if ((rope_cos == nullptr) != (rope_sin == nullptr) || (rope_cos != nullptr && rope_len <= 0))
+    return fail(FA_ERR_INVALID, "rotary tables cos/sin [L, D/2] required");
+  const AppendArgs app = {k_new, v_new, advance, start_pos, start_positions};
+  return paged_fwd(q, k_pages, v_pages, seqlen, page_size, head_map, o, B, Hq, M, D, NB, Hk, P,
+                   causal, q_offset, 0, q_offsets, nullptr, nullptr, block_table, max_blocks,
+                   heads_per_kv, workspace, workspace_bytes, rope_cos, rope_sin,
+                   rope_cos != nullptr ? rope_len : 0, stream, true, &app);
 }
 
 static int kv_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new, int B,

@@ -123,6 +123,18 @@ __global__ __launch_bounds__(256) void paged_append_rope_kernel(
   *reinterpret_cast<u32x4*>(v_pages + dst + half) = v2;
 }
 
+__global__ __launch_bounds__(256) void advance_lengths_kernel(int32_t* __restrict__ seqlen, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) seqlen[b] += 1;
+}
+
+hipError_t launch_advance_lengths(int32_t* seqlen, int B, hipStream_t stream) {
+  if (B <= 0) return hipSuccess;
+  hipLaunchKernelGGL(advance_lengths_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0,
+                     stream, seqlen, B);
+  return hipGetLastError();
+}
+
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
                                const int32_t* start_positions, const int32_t* token_positions,

@@ -124,6 +124,21 @@ struct AttnParams {
   // of each KV head's q heads into 128-row tiles, at most pack_heads heads
   // per KV head (fa_prefill.hip); 0 keeps one q head per tile
   int pack_heads;
+  // Append of one new token per (sequence, KV head) fused into the decode
+  // step (fa_flash_attn_paged_append_fwd). app_k / app_v [B, Hk, 1, D] go to
+  // position app_start(b) of the pages (k / v). The decode kernel takes the
+  // token's row from app_k / app_v in registers, and the combine kernel,
+  // which runs after every page read, writes it into the pages. With
+  // app_advance the position is seqlen[b] (the length before the append),
+  // the attention sees seqlen[b] + 1 keys, and the combine kernel stores
+  // seqlen[b] + 1. The kernels that take the step without the fused path
+  // (prefill path) also see seqlen[b] + 1 keys.
+  const f16* app_k;              // nullptr: no fused append
+  const f16* app_v;
+  const int32_t* app_positions;  // nullable [B]: start positions
+  int app_pos;                   // start position when app_positions is null
+  int app_advance;               // 0 or 1
+  int* ws_app;                   // [B] positions the decode kernel publishes to the combine kernel
 
   __device__ __forceinline__ int q_off(int b) const { return q_offsets ? q_offsets[b] : q_offset; }
   __device__ __forceinline__ int k_off(int b) const { return k_offsets ? k_offsets[b] : k_offset; }
@@ -136,9 +151,13 @@ struct AttnParams {
   // Number of keys of sequence b (clamped to the capacity).
   __device__ __forceinline__ int kv_len(int b) const {
     if (seqlen == nullptr) return N;
-    int n = seqlen[b];
+    int n = seqlen[b] + app_advance;
     n = n < 0 ? 0 : n;
     return n > N ? N : n;
+  }
+  // Position of the fused append's new token of sequence b.
+  __device__ __forceinline__ int app_start(int b) const {
+    return app_advance ? seqlen[b] : app_positions ? app_positions[b] : app_pos;
   }
   // K/V head of query head hq, or -1 if the head map points outside [0, Hk).
   __device__ __forceinline__ int kv_head(int hq) const {
@@ -220,5 +239,13 @@ constexpr int kSegmentCost = 12;
 // kernel; needs the workspace of plan_decode) or on the prefill kernel.
 constexpr int kPackedMinTiles = 256;
 bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv);
+// Whether a paged call with a fused append (one new token per sequence, no
+// rotary tables) runs the append inside the decode kernels: the decode path
+// with at most two 16-row blocks of query rows per KV head (the fused
+// variants keep the new token's fragments in registers beside them).
+bool fused_append_ok(int B, int M, int Hq, int Hk, int heads_per_kv);
+// seqlen[b] += 1 for b < B (the fused append's advance when the step does
+// not run on the fused decode kernels).
+hipError_t launch_advance_lengths(int32_t* seqlen, int B, hipStream_t stream);
 
 }  // namespace fa

@@ -198,9 +198,10 @@ __device__ __forceinline__ int key_groups(int keys) { return (keys + 15) >> 4; }
 // the prefix (two barriers, against seventeen for a 256-wide LDS scan: the
 // unit prefix is the first thing every workgroup does). The visible key limit
 // of each sequence is kept in s_keys[b] for the segments, so the key counts
-// are read from memory once per workgroup.
+// are read from memory once per workgroup. With the fused append, s_app[b]
+// keeps the new token's position of sequence b (read in the same round trip).
 __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, int* s_part,
-                                            int* s_keys) {
+                                            int* s_keys, int* s_app) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int chunk = (p.B + kDecodeThreads - 1) / kDecodeThreads;
@@ -209,6 +210,7 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
   for (int b = b0; b < b1; ++b) {
     const int keys = visible_keys(p, b);
     s_keys[b] = keys;
+    if (s_app != nullptr) s_app[b] = p.app_start(b);
     sum += key_groups(keys) * p.Hk;
   }
   int incl = sum;  // inclusive prefix of the chunk sums within the wave
@@ -321,7 +323,15 @@ __device__ __forceinline__ SplitRange split_range(const int* units, int B, int H
 // NBLK (1, 2 or 4): column blocks of 16 query rows served by one pass over
 // the segment's K/V. A KV head with more than 16 * NBLK query rows (heads x
 // positions) is walked once per 16 * NBLK rows.
-template <int D, bool ALIGNED, bool QSPLIT, int NBLK>
+//
+// APPEND (the fused append of fa_flash_attn_paged_append_fwd, without rotary
+// tables): the new token of (b, hk) at position s = app_start(b) is not read
+// from the pages, which the combine kernel writes only after this kernel. A
+// segment that holds s loads the lane's fragments of the token's K and V rows
+// before its group loop, and puts them into the group's registers in place of
+// the page row before the group is processed. Nothing here waits on the
+// append.
+template <int D, bool ALIGNED, bool QSPLIT, int NBLK, bool APPEND>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
   constexpr int DPL = DecodeRegs<D>::DPL;
@@ -333,6 +343,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   __shared__ int s_count;
   __shared__ int s_units[kMaxBatch + 1];
   __shared__ int s_keys[kMaxBatch];      // visible key limit per sequence
+  __shared__ int s_app[APPEND ? kMaxBatch : 1];  // fused append: new token's position
   __shared__ int s_part[kDecodeWaves];
   // Wave merge buffers: waves 2 and 3 hand their state to waves 0 and 1, which
   // then publish the pairwise merge (half the LDS of one slot per wave, so four
@@ -353,12 +364,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   // the unit prefix (Hq <= kMaxHeads = one head per thread), so a segment's
   // head scan below reads LDS instead of waiting on memory.
   const int my_hk = tid < p.Hq ? p.kv_head(tid) : -1;
-  unit_prefix(p, s_units, s_part, s_keys);
+  unit_prefix(p, s_units, s_part, s_keys, APPEND ? s_app : nullptr);
   s_hmap[tid] = my_hk;
   __syncthreads();
   const int U = s_units[p.B];
   if (w == 0) {
-    for (int b = tid; b <= p.B; b += kDecodeThreads) p.ws_units[b] = s_units[b];
+    for (int b = tid; b <= p.B; b += kDecodeThreads) {
+      p.ws_units[b] = s_units[b];
+      if (APPEND && b < p.B) p.ws_app[b] = s_app[b];
+    }
   }
   const int P = split_cost_p(p, U, W);
   const SplitRange range = split_range(s_units, p.B, p.Hk, U, W, P, w);
@@ -399,6 +413,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         QSPLIT ? (uint32_t)(2 * (p.kv.paged ? (int64_t)D : p.kv.stride_tok)) : 2u * D;
     const GroupLane<D> glane(n, quarter, row_bytes);
     const int g0 = g_begin + wave;
+
+    // Fused append: the group g_app of this range holding the new token (row
+    // r_app of it), or -1, and the lane's fragments of the token's K and V
+    // rows, loaded after the segment's first K/V groups and Q (they are
+    // needed only when their group comes up). The token replaces the page row
+    // only where some row sees it and where the append writes it (a mapped
+    // page, checked when the group comes up).
+    int g_app = -1, r_app = 0;
+    u32x4 app_k[APPEND ? KSTEPS : 1];
+    uint32_t app_v[APPEND ? VW : 1];
+    // The new token's row in place of the page's (group gi in ring slot r).
+    auto substitute = [&](DecodeRegs<D>& r, int gi) {
+      if constexpr (APPEND) {
+        if (gi != g_app) return;
+        // only where the append writes the token (a mapped page); the block
+        // table entry is the one the group's own loads looked up
+        if (p.kv.row_offset(b, hk, (g_app << 4) + r_app) < 0) return;
+        if (n == r_app) {
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk) r.k[kk] = app_k[kk];
+        }
+        if (quarter == (r_app >> 2)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (i == (r_app & 3)) {
+#pragma unroll
+              for (int w2 = 0; w2 < VW; ++w2) r.v[i][w2] = app_v[w2];
+            }
+          }
+        }
+      }
+    };
     // With ALIGNED loads every prefetch is issued unconditionally (groups past
     // the end read as empty ranges), which keeps the number of loads in flight
     // the same on every path, so each group waits only for its own loads.
@@ -572,6 +618,27 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         }
       };
 
+      // the new token's fragments (fused append; see g_app above)
+      if constexpr (APPEND) {
+        const int s = __builtin_amdgcn_readfirstlane(s_app[b]);
+        if (s >= 0 && s < t_end && (s >> 4) >= g_begin && (s >> 4) < g_end) {
+          g_app = s >> 4;
+          r_app = s & 15;
+          const int64_t row = ((int64_t)b * p.Hk + hk) * D;
+          // K: the lane's chunks 8*quarter + 32*kk of the row (row n of a group)
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk)
+            app_k[kk] = *reinterpret_cast<const u32x4*>(p.app_k + row + 8 * quarter + 32 * kk);
+          // V: the lane's DPL dims at DPL * n (of rows 4*quarter + i)
+          const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.app_v + row + DPL * n);
+#pragma unroll
+          for (int w2 = 0; w2 < VW; ++w2) app_v[w2] = vr[w2];
+        }
+        // wave-uniform, so that the group test and the page lookup of the
+        // substitution stay scalar
+        g_app = __builtin_amdgcn_readfirstlane(g_app);
+        r_app = __builtin_amdgcn_readfirstlane(r_app);
+      }
       for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
 #pragma unroll
         for (int i = 0; i < RING; ++i) {
@@ -581,6 +648,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           if (ALIGNED || gl < g_end)
             load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
                                    quarter, glane);
+          substitute(ring[i], gi);
           process(ring[i], gi << 4);
         }
       }
@@ -675,6 +743,43 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   }
 }
 
+
+// The fused append's page writes, done by workgroups of the combine grid of
+// their own (after the merge workgroups), so that their load -> page lookup
+// -> store chain runs beside the merge instead of before it; the combine
+// kernel runs after every read of the pages. Row (b, hk) of app_k / app_v
+// goes to position ws_app[b] of the pages, one 16-byte chunk per lane,
+// skipped where the page is not mapped or beyond the capacity, as
+// paged_append_kernel skips it. With app_advance, seqlen[b] becomes
+// ws_app[b] + 1. `first` and `nthreads` give this thread's lanes of the
+// grid-stride loop.
+template <int D>
+__device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t first,
+                                                    int64_t nthreads) {
+  f16* kd = reinterpret_cast<f16*>(const_cast<void*>(p.k));
+  f16* vd = reinterpret_cast<f16*>(const_cast<void*>(p.v));
+  constexpr int per_row = D / 8;
+  const int64_t total = (int64_t)p.B * p.Hk * per_row;
+  for (int64_t e = first; e < total; e += nthreads) {
+    const int64_t row = e / per_row;
+    const int c = (int)(e - row * per_row);
+    const int b = (int)(row / p.Hk);
+    const int hk = (int)(row - (int64_t)b * p.Hk);
+    const int pos = p.ws_app[b];
+    if (pos < 0) continue;
+    const int64_t dst = p.kv.row_offset(b, hk, pos);
+    if (dst < 0) continue;
+    *reinterpret_cast<u32x4*>(kd + dst + 8 * c) =
+        *reinterpret_cast<const u32x4*>(p.app_k + row * D + 8 * c);
+    *reinterpret_cast<u32x4*>(vd + dst + 8 * c) =
+        *reinterpret_cast<const u32x4*>(p.app_v + row * D + 8 * c);
+  }
+  if (p.app_advance) {
+    int32_t* sl = const_cast<int32_t*>(p.seqlen);
+    for (int64_t b = first; b < p.B; b += nthreads) sl[b] = p.ws_app[b] + 1;
+  }
+}
+
 // Merges the partials of one query row (one wave per row (b, hq, i)): the
 // workgroups whose unit range meets the row's segment are recomputed from the
 // unit prefix the decode kernel stored.
@@ -685,10 +790,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 template <int D, bool WIDE>
 __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   constexpr int DPW = D / 64;  // d values per lane
+  const int total = p.B * p.Hq * p.M;
+  const int merge_wgs = WIDE ? total : (total + 3) / 4;
+  if ((int)blockIdx.x >= merge_wgs) {
+    // the fused append's workgroups (launch_combine adds them)
+    const int64_t nthreads = (int64_t)(gridDim.x - merge_wgs) * blockDim.x;
+    fused_append_writes<D>(p, (int64_t)(blockIdx.x - merge_wgs) * blockDim.x + threadIdx.x,
+                           nthreads);
+    return;
+  }
   const int wave = threadIdx.x >> 6;
   const int row = WIDE ? (int)blockIdx.x : (int)blockIdx.x * 4 + wave;
   const int lane = threadIdx.x & 63;
-  const int total = p.B * p.Hq * p.M;
   if (row >= total) return;
   const int qi = row % p.M;
   const int hq = (row / p.M) % p.Hq;
@@ -708,7 +821,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   }
   const int ri = rank * p.M + qi;
   float result[DPW];
-  const int kv_len = p.kv_len(b);
+  // With the fused append's advance, this kernel advances seqlen: the key
+  // count comes from the position the decode kernel published.
+  const int kv_len = p.app_k != nullptr && p.app_advance ? min(max(p.ws_app[b] + 1, 0), p.N)
+                                                        : p.kv_len(b);
   if (qi >= p.q_len(b)) {
     // padding row (q_lens): zeros
 #pragma unroll
@@ -835,6 +951,7 @@ struct DecodeVariant {
   bool aligned;
   bool qsplit;
   int nblk;
+  bool append;  // fused append (at most two row blocks: fused_append_ok)
 };
 
 // Row blocks per pass: four (64 rows), except the per-row load variant at
@@ -854,23 +971,28 @@ DecodeVariant decode_variant(const AttnParams& p) {
                          : p.kv.stride_tok == p.kv.D;
   const int want = p.dec_rows <= kRows ? 1 : p.dec_rows <= 2 * kRows ? 2 : 4;
   v.nblk = v.qsplit ? 1 : std::min(want, max_row_blocks(p.kv.D, v.aligned));
+  v.append = p.app_k != nullptr;
   return v;
 }
 
 template <int D, bool ALIGNED>
-const void* decode_fn_rows(int nblk) {
+const void* decode_fn_rows(int nblk, bool append) {
   constexpr int NB4 = max_row_blocks(D, ALIGNED) >= 4 ? 4 : 2;
-  return nblk == 1 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 1>)
-       : nblk == 2 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 2>)
-                   : reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, NB4>);
+  if (append)
+    return nblk == 1 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 1, true>)
+                     : reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 2, true>);
+  return nblk == 1 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 1, false>)
+       : nblk == 2 ? reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, 2, false>)
+                   : reinterpret_cast<const void*>(&decode_kernel<D, ALIGNED, false, NB4, false>);
 }
 
 template <int D>
 const void* decode_fn(DecodeVariant v) {
   if (v.qsplit)
-    return v.aligned ? reinterpret_cast<const void*>(&decode_kernel<D, true, true, 1>)
-                     : reinterpret_cast<const void*>(&decode_kernel<D, false, true, 1>);
-  return v.aligned ? decode_fn_rows<D, true>(v.nblk) : decode_fn_rows<D, false>(v.nblk);
+    return v.aligned ? reinterpret_cast<const void*>(&decode_kernel<D, true, true, 1, false>)
+                     : reinterpret_cast<const void*>(&decode_kernel<D, false, true, 1, false>);
+  return v.aligned ? decode_fn_rows<D, true>(v.nblk, v.append)
+                   : decode_fn_rows<D, false>(v.nblk, v.append);
 }
 
 int decode_grid_wgs(int D, DecodeVariant var) {
@@ -882,11 +1004,12 @@ int decode_grid_wgs(int D, DecodeVariant var) {
   // unevenly (the older one is served first), so the younger half ends late,
   // and each workgroup's prologue and merge are paid over half the units.
   // A partial second round (e.g. 320 or 384 workgroups) is slower still.
-  static std::atomic<int> cache[64][32];
+  static std::atomic<int> cache[64][64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   const int blk = var.nblk == 1 ? 0 : var.nblk == 2 ? 1 : 2;
-  const int idx = (D == 128 ? 16 : 0) + blk * 4 + (var.qsplit ? 2 : 0) + (var.aligned ? 1 : 0);
+  const int idx = (var.append ? 32 : 0) + (D == 128 ? 16 : 0) + blk * 4 + (var.qsplit ? 2 : 0) +
+                  (var.aligned ? 1 : 0);
   int v = cache[dev][idx].load(std::memory_order_relaxed);
   if (v > 0) return v;
   int cus = 0, per_cu = 0;
@@ -925,6 +1048,12 @@ bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv) {
   return rows <= 4 * kRows || (packable && rows <= 16 * kRows);
 }
 
+bool fused_append_ok(int B, int M, int Hq, int Hk, int heads_per_kv) {
+  if (!use_decode_path(B, M, Hq, Hk, heads_per_kv)) return false;
+  const int64_t hpk = heads_per_kv <= 0 || heads_per_kv > Hq ? Hq : heads_per_kv;
+  return hpk * M <= 2 * kRows;
+}
+
 int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
   if (getenv("FA_DECODE_WGS") != nullptr) return plan.wgs;
   const int r = decode_grid_wgs(D, decode_variant(p));
@@ -947,20 +1076,28 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
   const size_t slots = (size_t)B * Hk + (size_t)plan.wgs;
   plan.o_bytes = (slots * plan.rows * D * sizeof(float) + 255) / 256 * 256;
   plan.ml_bytes = (slots * plan.rows * 2 * sizeof(float) + 255) / 256 * 256;
-  plan.ws_bytes = plan.o_bytes + plan.ml_bytes + (size_t)(B + 1) * sizeof(int);
+  // unit prefix [B + 1], then the fused append's positions [B]
+  plan.ws_bytes = plan.o_bytes + plan.ml_bytes + (size_t)(2 * B + 1) * sizeof(int);
   return plan;
 }
 
 // Rows with many partial slots (few rows: one long sequence, or a few) merge
 // with a workgroup per row; otherwise a wave per row.
+// With the fused append, workgroups for its page writes follow the merge
+// workgroups in the same grid (one lane per chunk, at most 1024 workgroups).
 template <int D>
 void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
+  int64_t app_wgs = 0;
+  if (p.app_k != nullptr) {
+    const int64_t lanes = (int64_t)p.B * p.Hk * (D / 8);
+    app_wgs = std::min<int64_t>(1024, std::max<int64_t>(1, (lanes + 255) / 256));
+  }
   if (rows <= 512)
-    hipLaunchKernelGGL((decode_combine_kernel<D, true>), dim3((unsigned)rows), dim3(256), 0, stream,
-                       p);
-  else
-    hipLaunchKernelGGL((decode_combine_kernel<D, false>), dim3((unsigned)((rows + 3) / 4)),
+    hipLaunchKernelGGL((decode_combine_kernel<D, true>), dim3((unsigned)(rows + app_wgs)),
                        dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<D, false>),
+                       dim3((unsigned)((rows + 3) / 4 + app_wgs)), dim3(256), 0, stream, p);
 }
 
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {

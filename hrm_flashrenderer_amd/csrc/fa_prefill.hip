@@ -389,7 +389,7 @@ __device__ __forceinline__ int ld_or(const int32_t* ptr, int idx, int dflt, cons
 
 __device__ __forceinline__ SeqData seq_data(const AttnParams& p, int b, int hq) {
   SeqData d;
-  const int n = ld_or(p.seqlen, b, p.N, p.q);
+  const int n = ld_or(p.seqlen, b, p.N, p.q) + (p.seqlen != nullptr ? p.app_advance : 0);
   d.kv_len = n < 0 ? 0 : n > p.N ? p.N : n;
   const int hk = ld_or(p.head_map, hq, p.head_mod ? hq % p.Hk : hq / p.group, p.q);
   d.hk = (hk >= 0 && hk < p.Hk) ? hk : -1;

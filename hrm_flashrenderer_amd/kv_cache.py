@@ -47,7 +47,7 @@ from typing import List, Optional, Sequence, Tuple, Union
 import numpy as np
 import torch
 
-from .ops import flash_attn_paged, paged_kv_append, paged_kv_scatter
+from .ops import flash_attn_paged, flash_attn_paged_append, paged_kv_append, paged_kv_scatter
 
 PositionsLike = Union[None, int, torch.Tensor]
 
@@ -361,6 +361,31 @@ class PagedKVCache:
         return flash_attn_paged(q, self.k_pages, self.v_pages, self.seqlen, self.page_size,
                                 head_map, causal, q_offset, 0, block_table=self._block_table,
                                 rope=rope, q_lens=q_lens)
+
+    def decode_step(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                    head_map: torch.Tensor, *, causal: bool = False, rope=None) -> torch.Tensor:
+        """One decode step in one call: append k_new / v_new `[B, Hk, 1, D]` at
+        every sequence's current length and attend with q `[B, Hq, M, D]`
+        over the lengths that include the new token.
+
+        The same as `append(k_new, v_new)` then `attention(q, head_map,
+        causal, q_offset=lengths, rope=rope)` (the reference's decode step,
+        engine/llama_tp.py:183-200), but the lengths advance on the device and
+        the append needs no launch of its own when the attention runs on the
+        decode kernels without rope (see flash_attn_paged_append). The query
+        rows sit at the new token's position (q_offset = the lengths before
+        the step).
+        """
+        B, Hk, T, D = k_new.shape
+        if B != self.bsz or Hk != self.kv_heads or D != self.head_dim or T != 1:
+            raise ValueError("k_new must be [bsz, kv_heads, 1, head_dim]")
+        self._reserve_many([(b, -(-(n + 1) // self.page_size)) for b, n in enumerate(self.lengths)])
+        o = flash_attn_paged_append(q, self.k_pages, self.v_pages, k_new.contiguous(),
+                                    v_new.contiguous(), self.seqlen, self.page_size, head_map,
+                                    causal, block_table=self._block_table, rope=rope)
+        self.lengths = [n + 1 for n in self.lengths]
+        self.cur_len = max(self.lengths)
+        return o
 
     def prefill_chunk(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                       starts: Sequence[int], valid: Sequence[int], head_map: torch.Tensor,

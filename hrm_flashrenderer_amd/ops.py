@@ -240,6 +240,41 @@ def _(k_pages, v_pages, k_new, v_new, start_pos, start_positions, page_size, blo
     return None
 
 
+@torch.library.custom_op("hrm_fa::flash_attn_paged_append",
+                         mutates_args=("k_pages", "v_pages", "seqlen"))
+def _flash_attn_paged_append_op(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                                seqlen: torch.Tensor, page_size: int, head_map: torch.Tensor,
+                                causal: bool, q_offset: int, q_offsets: Optional[torch.Tensor],
+                                block_table: Optional[torch.Tensor], k_new: torch.Tensor,
+                                v_new: torch.Tensor, advance: bool, start_pos: int,
+                                start_positions: Optional[torch.Tensor],
+                                rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor],
+                                heads_per_kv: int = 0) -> torch.Tensor:
+    lib = _lib.load()
+    o = torch.empty_like(q)
+    B, Hq, M, D = q.shape
+    NB, Hk, P = k_pages.size(0), k_pages.size(1), k_pages.size(2)
+    max_blocks = int(block_table.size(1)) if block_table is not None else 0
+    cap_pages = max_blocks if block_table is not None else P
+    ws_bytes = lib.fa_paged_workspace_bytes(B, Hq, M, D, Hk, cap_pages, page_size, heads_per_kv)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    with _DeviceScope(q) as stream:
+        _lib.check(lib.fa_flash_attn_paged_append_fwd(
+            q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), seqlen.data_ptr(), page_size,
+            head_map.data_ptr(), o.data_ptr(), B, Hq, M, D, NB, Hk, P, int(causal), q_offset,
+            _ptr(q_offsets), _ptr(block_table), max_blocks, heads_per_kv, k_new.data_ptr(),
+            v_new.data_ptr(), int(advance), start_pos, _ptr(start_positions), _ptr(rope_cos),
+            _ptr(rope_sin), rope_cos.size(0) if rope_cos is not None else 0, _ptr(ws), ws_bytes,
+            stream))
+    return o
+
+
+@_flash_attn_paged_append_op.register_fake
+def _(q, k_pages, v_pages, seqlen, page_size, head_map, causal, q_offset, q_offsets, block_table,
+      k_new, v_new, advance, start_pos, start_positions, rope_cos, rope_sin, heads_per_kv=0):
+    return torch.empty_like(q)
+
+
 @torch.library.custom_op("hrm_fa::paged_kv_scatter", mutates_args=("k_pages", "v_pages"))
 def _paged_kv_scatter_op(k_pages: torch.Tensor, v_pages: torch.Tensor, k_new: torch.Tensor,
                          v_new: torch.Tensor, positions: torch.Tensor, page_size: int,
@@ -429,6 +464,60 @@ def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, blo
                    f"positions {sp}..{sp + k_new.size(2) - 1} are outside the rotary table "
                    f"of {cos.size(0)}")
     _paged_kv_append_op(k_pages, v_pages, k_new, v_new, sp, sp_t, page_size, block_table, cos, sin)
+
+
+def flash_attn_paged_append(q, k_pages, v_pages, k_new, v_new, seqlen, page_size, head_map,
+                            causal=False, q_offset=None, *, start_pos=None, block_table=None,
+                            rope=None):
+    """One decode step in one call: `paged_kv_append` of one new token per
+    sequence, then `flash_attn_paged` over the pages that now hold it; returns
+    the attention output shaped like q.
+
+    The reference's decode step makes these two calls (cache.append,
+    engine/llama_tp.py:65-78, then flash_attn_paged, :186-200). Here, when the
+    attention runs on the decode kernels with at most 32 query rows per KV
+    head (single-token decode at the benchmark shapes) and without rope, the
+    append has no launch of its own: the decode kernel reads the new token from k_new /
+    v_new and its merge kernel writes it into the pages. Other shapes launch
+    the append kernel first. Results equal the two calls' in every case.
+
+    k_new, v_new: fp16 [B, Hk, 1, D] (written into the pages in place).
+    start_pos=None: the token of sequence b goes to position seqlen[b], the
+        attention sees seqlen[b] + 1 keys, and seqlen is advanced by one on
+        the device (the reference's update, llama_tp.py:77); q_offset
+        defaults to seqlen (the query at the new token's position; only
+        causal attention and rope read it).
+    start_pos=int or int32 [B] tensor: the token goes there, and seqlen
+        already counts it; q_offset defaults to 0, as in flash_attn_paged.
+    rope=(cos, sin): K is rotated at its position as paged_kv_append(rope=)
+        does, and q at q_offset + i as flash_attn_paged(rope=) does.
+    """
+    page_size = int(page_size)
+    validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
+    advance = start_pos is None
+    sp, sp_t = validate_paged_kv_append(k_pages, v_pages, k_new, v_new, 0 if advance else start_pos,
+                                        page_size, block_table)
+    _check(k_new.size(0) == q.size(0), "B mismatch")
+    _check(k_new.size(2) == 1, "k_new/v_new [B, Hk, 1, D]: one new token per sequence")
+    _check(k_new.size(3) == q.size(3), "D mismatch")
+    B = q.size(0)
+    if q_offset is None:
+        q_offset = seqlen if advance else 0
+    qo, qo_t = _per_seq(q_offset, B, "q_offset", q.device)
+    cos, sin = _check_rope(rope, q.size(3), q.device)
+    if cos is not None:
+        _check(q.size(3) % 16 == 0, "rotary append needs head_dim a multiple of 16")
+        if not advance and sp_t is None:
+            _check(0 <= sp < cos.size(0),
+                   f"position {sp} is outside the rotary table of {cos.size(0)}")
+        if qo_t is None and q.size(2) > 0:
+            _check(qo >= 0 and qo + q.size(2) <= cos.size(0),
+                   f"positions {qo}..{qo + q.size(2) - 1} are outside the rotary table "
+                   f"of {cos.size(0)}")
+    hpk = heads_per_kv(head_map, k_pages.size(1))
+    return _flash_attn_paged_append_op(q, k_pages, v_pages, seqlen, page_size, head_map,
+                                       bool(causal), qo, qo_t, block_table, k_new, v_new,
+                                       advance, sp, sp_t, cos, sin, hpk)
 
 
 def paged_kv_scatter(k_pages, v_pages, k_new, v_new, positions, page_size, *, block_table=None,

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 /* element type of q / k / v / o */
 #define FA_DTYPE_F16 0
@@ -146,7 +146,7 @@ int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const vo
  * heads_per_kv bound. It depends only on host-known sizes (the per-sequence
  * capacity in pages is P, or max_blocks when a block table is used), never on
  * device contents: (B*Hk + W) slots x heads_per_kv*M rows x (D + 2) fp32, W
- * the decode workgroup count (<= 1024), plus B + 1 ints.
+ * the decode workgroup count (<= 1024), plus 2*B + 1 ints.
  */
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk,
                                 int capacity_pages, int page_size, int heads_per_kv);
@@ -228,6 +228,46 @@ int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const v
                         const int32_t* positions, const int32_t* block_table, int max_blocks,
                         const void* rope_cos, const void* rope_sin, int rope_len,
                         void* stream);
+
+/*
+ * One decode step: the append of one new token per sequence and the paged
+ * attention over the pages that hold it, in one call. Replaces the pair of
+ * calls the reference's decode step makes, cache.append (engine/llama_tp.py:
+ * 65-78 -> _ext.paged_kv_append, csrc/ext.cpp:70-89) then flash_attn_paged
+ * (engine/llama_tp.py:186-200 -> csrc/ext.cpp:42-68), with the same results:
+ * it equals fa_paged_kv_append(_rope) with T = 1 followed by
+ * fa_flash_attn_paged(_rope)_fwd (k_offset 0, no q_lens).
+ *   k_new, v_new : fp16 [B, Hk, 1, D], written into the pages in place.
+ *   advance = 0 : the token of sequence b goes to position start_positions[b]
+ *                 (or start_pos); seqlen already counts it.
+ *   advance = 1 : it goes to position seqlen[b] (start_pos 0, start_positions
+ *                 NULL), the attention sees seqlen[b] + 1 keys, and seqlen[b]
+ *                 is advanced by one on the device after the attention (the
+ *                 reference's seqlen update after the append, llama_tp.py:77).
+ *                 For the decode query at the new token's position, pass
+ *                 q_offsets = seqlen (read before the advance).
+ *   rope_cos, rope_sin : both NULL, or the rotary tables of
+ *                 fa_flash_attn_paged_rope_fwd: K is rotated at its position
+ *                 as fa_paged_kv_append_rope does, Q at q_off(b) + i.
+ *   workspace : as for fa_flash_attn_paged_fwd (fa_paged_workspace_bytes).
+ * When the attention runs on the decode kernels with at most 32 query rows
+ * per KV head (heads_per_kv * M <= 32: single-token decode at the benchmark
+ * shapes) and without rotary tables, the append costs no launch of its own: the decode kernel takes
+ * the new token's row from k_new / v_new, and its merge kernel, which runs
+ * after every page read, writes the row into the pages (and advances
+ * seqlen). Other shapes run the append kernel, then the attention (then the
+ * advance). No counterpart in the reference, which launches the two
+ * separately.
+ */
+int fa_flash_attn_paged_append_fwd(const void* q, void* k_pages, void* v_pages, int32_t* seqlen,
+                                   int page_size, const int32_t* head_map, void* o,
+                                   int B, int Hq, int M, int D, int NB, int Hk, int P,
+                                   int causal, int64_t q_offset, const int32_t* q_offsets,
+                                   const int32_t* block_table, int max_blocks, int heads_per_kv,
+                                   const void* k_new, const void* v_new, int advance,
+                                   int64_t start_pos, const int32_t* start_positions,
+                                   const void* rope_cos, const void* rope_sin, int rope_len,
+                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Single-sequence decode attention over a token-major fp16 KV cache: the

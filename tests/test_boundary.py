@@ -31,7 +31,8 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "fa_abi_version", "fa_decode_token_major", "fa_decode_token_major_workspace_bytes",
-        "fa_flash_attn_fwd", "fa_flash_attn_paged_fwd", "fa_flash_attn_paged_fwd_noalloc",
+        "fa_flash_attn_fwd", "fa_flash_attn_paged_append_fwd", "fa_flash_attn_paged_fwd",
+        "fa_flash_attn_paged_fwd_noalloc",
         "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
         "fa_paged_kv_append_rope", "fa_paged_kv_scatter", "fa_paged_workspace_bytes"])
 
@@ -46,6 +47,29 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def _status_and_message(rc):
     return rc, _lib.load().fa_last_error().decode()
+
+
+def test_fused_append_entry_rejects_bad_arguments_without_a_device():
+    """fa_flash_attn_paged_append_fwd validates before it launches anything."""
+    lib = _lib.load()
+    P = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+
+    def call(advance=1, start_pos=0, start_positions=None, cos=None, sin=None, rope_len=0, D=128,
+             NB=2, page_size=16):
+        return _status_and_message(lib.fa_flash_attn_paged_append_fwd(
+            P, P, P, P, page_size, P, P, 2, 8, 1, D, NB, 2, 4, 0, 0, None, None, 0, 4, P, P,
+            advance, start_pos, start_positions, cos, sin, rope_len, None, 0, None))
+
+    assert call(advance=2) == (-1, "advance must be 0 or 1")
+    assert call(advance=1, start_pos=3) == (
+        -1, "with advance the positions are the lengths: no start positions")
+    assert call(advance=1, start_positions=P) == (
+        -1, "with advance the positions are the lengths: no start positions")
+    assert call(cos=P, sin=None, rope_len=8) == (-1, "rotary tables cos/sin [L, D/2] required")
+    assert call(cos=P, sin=P, rope_len=0) == (-1, "rotary tables cos/sin [L, D/2] required")
+    assert call(D=96) == (-1, "Supported head_dim: 64 or 128")
+    assert call(NB=3) == (-1, "B mismatch")
+    assert call(page_size=0) == (-1, "page_size mismatch")
 
 
 def test_c_abi_rejects_bad_arguments_without_a_device():
@@ -123,7 +147,8 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
 def test_workspace_sizing_depends_on_sizes_only():
     lib = _lib.load()
     # decode (M = 1): partial slots (B*Hk + workgroups) x (heads_per_kv*M rows)
-    # x (D + 2) floats (two 256-byte aligned parts) + the (B + 1) unit prefix;
+    # x (D + 2) floats (two 256-byte aligned parts) + the (B + 1) unit prefix
+    # and the B positions of the fused append;
     # 1024 workgroups unless a batch has fewer than 8 groups of 16 keys per
     # workgroup. A slot holds one KV head's query rows: cfg4's 64/8 heads need
     # 8 rows per slot (6.3 MB), against 64 with no bound (50 MB).
@@ -131,13 +156,13 @@ def test_workspace_sizing_depends_on_sizes_only():
     slots = 64 * 8 + 1024
     for hpk, rows in ((8, 8), (0, 64), (-3, 64), (100, 64), (5, 5)):
         ws = lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16, hpk)
-        assert ws == align(slots * rows * 128 * 4) + align(slots * rows * 2 * 4) + 65 * 4, hpk
+        assert ws == align(slots * rows * 128 * 4) + align(slots * rows * 2 * 4) + 129 * 4, hpk
     assert lib.fa_paged_workspace_bytes(64, 64, 1, 128, 8, 1025, 16, 8) < 7_000_000
     # M = 4 query rows per sequence and 5 heads per KV head: 20 rows per slot
     ws = lib.fa_paged_workspace_bytes(64, 40, 4, 128, 8, 1025, 16, 5)
-    assert ws == align(slots * 20 * 128 * 4) + align(slots * 20 * 2 * 4) + 65 * 4
+    assert ws == align(slots * 20 * 128 * 4) + align(slots * 20 * 2 * 4) + 129 * 4
     small = lib.fa_paged_workspace_bytes(1, 8, 1, 64, 8, 2, 16, 1)  # 16 units -> 2 workgroups
-    assert small == align((8 + 2) * 1 * 64 * 4) + align((8 + 2) * 1 * 2 * 4) + 2 * 4
+    assert small == align((8 + 2) * 1 * 64 * 4) + align((8 + 2) * 1 * 2 * 4) + 3 * 4
     # prefill-shaped calls need no workspace
     assert lib.fa_paged_workspace_bytes(4, 40, 2048, 128, 8, 128, 16, 5) == 0
     assert lib.fa_paged_workspace_bytes(1, 8, 1, 96, 8, 4, 16, 1) == 0
@@ -157,9 +182,9 @@ def test_workspace_sizing_depends_on_sizes_only():
     t_max = 4095  # 256 groups x 8 KV heads = 2048 units -> 256 workgroups
     slots = 8 + 256
     ws = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 5)
-    assert ws == align(slots * 5 * 128 * 4) + align(slots * 5 * 2 * 4) + 2 * 4
+    assert ws == align(slots * 5 * 128 * 4) + align(slots * 5 * 2 * 4) + 3 * 4
     ws0 = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 0)   # no bound: H rows
-    assert ws0 == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 2 * 4
+    assert ws0 == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 3 * 4
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100, 5) < ws
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max, 5) == 0
 

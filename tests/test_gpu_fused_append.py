@@ -1,0 +1,199 @@
+"""GPU parity of the fused decode step (flash_attn_paged_append,
+fa_flash_attn_paged_append_fwd) against the two calls it replaces.
+
+The reference's decode step appends the new token (cache.append,
+engine/llama_tp.py:65-78) and then runs flash_attn_paged over the cache
+(:186-200). The fused call must give the same bits: the attention output,
+every page of both pools (NaN-poisoned dead slots included, compared as raw
+bits) and, in advance mode, the lengths. The new token's own slot holds NaN
+before the step, so a kernel that read it from the pages instead of from
+k_new / v_new would produce NaN rows. Both outputs are also held to the fp64
+oracle at the fp32-softmax bar.
+
+Shapes: 8 and 32 query rows per KV head (the fused decode kernels: one and
+two 16-row blocks), 64 rows (decode kernels with four blocks, so the append
+kernel runs first) and 128-row prefill chunks (prefill path); D = 64 and 128;
+the rotary variant (append kernel first, then the rotary attention); new
+tokens at every place in a 16-key group and at page boundaries; an empty
+sequence (one key after the step).
+"""
+import pytest
+import torch
+
+from hrm_flashrenderer_amd import (PagedKVCache, build_rope_cache, flash_attn_paged,
+                                   flash_attn_paged_append, paged_kv_append)
+from paged_ref import assert_close, gather_seq, paged_reference, poison_dead_slots, seeded
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _setup(B, Hq, Hk, D, PS, old_lengths, seed, spare=6):
+    """Pool over a permuted block table, mapped for old length + 1 tokens,
+    slots past the old lengths NaN (the new token's slot included)."""
+    g = torch.Generator().manual_seed(seed)
+    new_lengths = [n + 1 for n in old_lengths]
+    pages = [(n + PS - 1) // PS for n in new_lengths]
+    total = sum(pages) + spare
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    mb = max(pages) + 1
+    bt = torch.full((B, mb), -1, dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[pos:pos + n]
+        pos += n
+    kp = seeded((1, Hk, total, PS, D), seed + 1)
+    vp = seeded((1, Hk, total, PS, D), seed + 2)
+    poison_dead_slots(kp, vp, bt, old_lengths, PS)
+    k_new = seeded((B, Hk, 1, D), seed + 3)
+    v_new = seeded((B, Hk, 1, D), seed + 4)
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(DEV)
+    return kp, vp, bt.to(DEV), k_new, v_new, hm
+
+
+def _bits(t):
+    return t.view(torch.int16)
+
+
+@pytest.mark.parametrize("advance", [False, True])
+@pytest.mark.parametrize("Hq,Hk,M,D,causal,rope", [
+    (64, 8, 1, 128, False, False),   # cfg4's step: 8 rows per KV head (fused, one block)
+    (40, 8, 1, 128, False, True),    # cfg3's heads, rotary
+    (32, 8, 8, 128, True, False),    # 32 rows per KV head (fused, two blocks)
+    (16, 4, 1, 64, False, False),    # D = 64
+    (16, 4, 8, 64, True, True),      # D = 64, two blocks, rotary
+    (64, 8, 8, 128, True, False),    # 64 rows per KV head: append kernel, then decode
+])
+def test_fused_step_matches_append_then_attention(gpu, advance, Hq, Hk, M, D, causal, rope):
+    PS = 16
+    old = [0, 15, 16, 31, 100, 1000, 47]   # new token at group offsets 0, 15, 0, 15, 4, 8, 15
+    B = len(old)
+    seed = 9100 + Hq + 7 * M + D + int(rope) + 2 * int(advance)
+    kp, vp, bt, k_new, v_new, hm = _setup(B, Hq, Hk, D, PS, old, seed)
+    q = seeded((B, Hq, M, D), seed + 5)
+    ropet = build_rope_cache(2048, D, device=DEV) if rope else None
+    old_t = torch.tensor(old, dtype=torch.int32, device=DEV)
+    new_t = old_t + 1
+    # the query rows sit at the last M positions (row M-1 at the new token):
+    # the causal limits and the rotary positions of q
+    qo = torch.clamp(new_t - M, min=0)
+
+    # reference: the two calls
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, old_t, PS, block_table=bt, rope=ropet)
+    o_ref = flash_attn_paged(q, kr, vr, new_t, PS, hm, causal, qo, block_table=bt, rope=ropet)
+
+    kf, vf = kp.clone(), vp.clone()
+    if advance:
+        sl = old_t.clone()
+        o = flash_attn_paged_append(q, kf, vf, k_new, v_new, sl, PS, hm, causal, q_offset=qo,
+                                    block_table=bt, rope=ropet)
+    else:
+        sl = new_t.clone()
+        o = flash_attn_paged_append(q, kf, vf, k_new, v_new, sl, PS, hm, causal, qo,
+                                    start_pos=old_t, block_table=bt, rope=ropet)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref)), "output differs from append + attention"
+    assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr)), "pages differ"
+    assert torch.equal(sl, new_t)
+    assert not torch.isnan(o).any()
+    if not rope:
+        ref = paged_reference(q, kr, vr, bt, [n + 1 for n in old], PS, hm, causal,
+                              qo.tolist() if causal else None)
+        on = o.cpu().numpy()
+        for (b, h), r in ref.items():
+            assert_close(on[b, h], r, f"b={b} h={h}")
+
+
+@pytest.mark.parametrize("advance", [False, True])
+def test_fused_step_prefill_path(gpu, advance):
+    """128 query rows per sequence run on the prefill kernel: the append kernel
+    runs first, then the attention sees the new token (and the advance)."""
+    B, Hq, Hk, M, D, PS = 3, 8, 2, 128, 128, 16
+    old = [200, 300, 511]
+    kp, vp, bt, k_new, v_new, hm = _setup(B, Hq, Hk, D, PS, old, 9300 + int(advance))
+    q = seeded((B, Hq, M, D), 9310)
+    old_t = torch.tensor(old, dtype=torch.int32, device=DEV)
+    new_t = old_t + 1
+    qo = new_t - M
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, old_t, PS, block_table=bt)
+    o_ref = flash_attn_paged(q, kr, vr, new_t, PS, hm, True, qo, block_table=bt)
+    kf, vf = kp.clone(), vp.clone()
+    sl = old_t.clone() if advance else new_t.clone()
+    o = flash_attn_paged_append(q, kf, vf, k_new, v_new, sl, PS, hm, True, qo,
+                                start_pos=None if advance else old_t, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref))
+    assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr))
+    assert torch.equal(sl, new_t)
+
+
+def test_fused_step_scalar_position_and_unmapped_page(gpu):
+    """A scalar position, and a per-sequence position whose page is not mapped
+    (the append skips it, as paged_kv_append does, and the attention reads
+    that position from the pool as the two calls would)."""
+    B, Hq, Hk, D, PS = 4, 16, 2, 128, 16
+    old = [63, 63, 63, 63]
+    kp, vp, bt, k_new, v_new, hm = _setup(B, Hq, Hk, D, PS, old, 9400)
+    q = seeded((B, Hq, 1, D), 9401)
+    new_t = torch.full((B,), 64, dtype=torch.int32, device=DEV)
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, 63, PS, block_table=bt)
+    o_ref = flash_attn_paged(q, kr, vr, new_t, PS, hm, False, block_table=bt)
+    kf, vf = kp.clone(), vp.clone()
+    o = flash_attn_paged_append(q, kf, vf, k_new, v_new, new_t.clone(), PS, hm, False, 0,
+                                start_pos=63, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref)) and torch.equal(_bits(kf), _bits(kr))
+    # sequence 2's new token in a page that is not mapped (entry -1): both
+    # skip the write, and both read that page's keys as zeros
+    bt2 = bt.clone()
+    bt2[2, 3] = -1
+    pos = torch.full((B,), 63, dtype=torch.int32, device=DEV)
+    seq = new_t
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, pos, PS, block_table=bt2)
+    o_ref = flash_attn_paged(q, kr, vr, seq, PS, hm, False, block_table=bt2)
+    kf, vf = kp.clone(), vp.clone()
+    o = flash_attn_paged_append(q, kf, vf, k_new, v_new, seq.clone(), PS, hm, False, 0,
+                                start_pos=pos, block_table=bt2)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref))
+    assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr))
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_cache_decode_steps_match_append_and_attention(gpu, rope):
+    """PagedKVCache.decode_step, three steps in a row after a ragged prefill,
+    against the cache's append() + attention() on a twin cache."""
+    B, Hq, Hk, D = 5, 40, 8, 128
+    ropet = build_rope_cache(4096, D, device=DEV) if rope else None
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(DEV)
+    fused = PagedKVCache(B, Hk, D, page_size=16, device=DEV, max_seq_len=2048)
+    twin = PagedKVCache(B, Hk, D, page_size=16, device=DEV, max_seq_len=2048)
+    lengths = [1, 17, 100, 255, 640]
+    k = seeded((B, Hk, max(lengths), D), 9500)
+    v = seeded((B, Hk, max(lengths), D), 9600)
+    for cache in (fused, twin):
+        cache.append(k, v, None, rope=ropet, valid=lengths)   # ragged prompts from position 0
+    for step in range(3):
+        q = seeded((B, Hq, 1, D), 9700 + step)
+        kn = seeded((B, Hk, 1, D), 9800 + step)
+        vn = seeded((B, Hk, 1, D), 9900 + step)
+        before = twin.seqlen.clone()
+        twin.append(kn, vn, rope=ropet)
+        o_ref = twin.attention(q, hm, False, before, rope=ropet)
+        o = fused.decode_step(q, kn, vn, hm, rope=ropet)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(o), _bits(o_ref)), f"step {step}"
+        assert fused.lengths == twin.lengths
+        assert torch.equal(fused.seqlen, twin.seqlen)
+    # every live row (slots no call wrote hold whatever the pool allocation held)
+    for cache_pool, twin_pool in ((fused.k_pages, twin.k_pages), (fused.v_pages, twin.v_pages)):
+        fc, tc = cache_pool.cpu(), twin_pool.cpu()
+        fbt, tbt = fused.block_table.cpu(), twin.block_table.cpu()
+        for b, n in enumerate(fused.lengths):
+            a = gather_seq(fc, fbt[b], n, 16)
+            r = gather_seq(tc, tbt[b], n, 16)
+            assert torch.equal(_bits(a), _bits(r)), f"sequence {b}"
