@@ -252,12 +252,14 @@ int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const v
  *   workspace : as for fa_flash_attn_paged_fwd (fa_paged_workspace_bytes).
  * When the attention runs on the decode kernels with at most 32 query rows
  * per KV head (heads_per_kv * M <= 32: single-token decode at the benchmark
- * shapes) and without rotary tables, the append costs no launch of its own: the decode kernel takes
- * the new token's row from k_new / v_new, and its merge kernel, which runs
- * after every page read, writes the row into the pages (and advances
- * seqlen). Other shapes run the append kernel, then the attention (then the
- * advance). No counterpart in the reference, which launches the two
- * separately.
+ * shapes) and without rotary tables, the append costs no launch of its own:
+ * the decode kernel takes the new token's row from k_new / v_new, and its
+ * merge kernel, which runs after every page read, writes the row into the
+ * pages (and advances seqlen). Other shapes run the append kernel, then the
+ * attention (then the advance). The results equal the two calls' as long as
+ * no sequence reads a page row that another sequence's new token is written
+ * to (pages shared between sequences are read-only to both). No counterpart
+ * in the reference, which launches the two separately.
  */
 int fa_flash_attn_paged_append_fwd(const void* q, void* k_pages, void* v_pages, int32_t* seqlen,
                                    int page_size, const int32_t* head_map, void* o,
