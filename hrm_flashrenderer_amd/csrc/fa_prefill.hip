@@ -326,7 +326,8 @@ __global__ __launch_bounds__(kThreads) void prefill_f16_kernel(AttnParams p) {
 //    the tile (16 or 8 keys), which lies in one page, through one buffer
 //    resource whose size covers only the slab's valid rows: rows past seqlen
 //    land in LDS as zeros.
-//  * LDS holds two K and two V tiles (double buffer, one barrier per tile).
+//  * LDS holds two K and two V tiles (double buffer, one barrier per tile;
+//    three of each for the packed rows, see the kernel).
 //    Rows are 2*D bytes; 16-byte chunks are XOR-swizzled per row so that the
 //    reads below are free of bank conflicts: K chunk c of row r is stored at
 //    c ^ (r % CH) (32 rows read at one column by ds_read_b128), V chunk c at
@@ -425,13 +426,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // compiler does not track it: it puts an `s_waitcnt vmcnt(0)` in front of
 // every ds_read_b64_tr_b16 that follows a DMA it knows of, which would make
 // each wave wait for its next tile's DMA before reading V of the current one.
-// Ordering is explicit instead: every DMA is waited for (vmcnt(0)) before the
+// Ordering is explicit instead: every DMA is waited for (vmcnt) before the
 // barrier that precedes the reads of its stage. The `s_nop 0` is the wait
-// state an LDS DMA needs after an SALU write of M0.
+// state an LDS DMA needs after an SALU write of M0. NT sets the non-temporal
+// cache policy, for K/V that no other workgroup reads.
+template <bool NT>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voffset), "s"(r), "{m0}"(m0) : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                 :: "v"(voffset), "s"(r), "{m0}"(m0) : "memory");
+  else
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voffset), "s"(r), "{m0}"(m0) : "memory");
 }
 
 template <int D>
@@ -592,14 +599,14 @@ __device__ __forceinline__ SlabLane<D, NW, BN> slab_lane(int wave, int lane) {
   return d;
 }
 
-template <int D, int NW, int BN>
+template <int D, int NW, int BN, bool NT>
 __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* voffs,
                                          const char* base, int wave, char* dst_tile) {
   using C = DmaCfg<D>;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(base + q.off * 2, q.nbytes);
 #pragma unroll
   for (int i = 0; i < Slab<D, NW, BN>::IPW; ++i)
-    lds_dma16(r, dst_tile + (Slab<D, NW, BN>::SLAB * wave + C::RPI * i) * C::ROWB, voffs[i]);
+    lds_dma16<NT>(r, dst_tile + (Slab<D, NW, BN>::SLAB * wave + C::RPI * i) * C::ROWB, voffs[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -626,7 +633,16 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   constexpr int TILE = BN * C::ROWB;
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
-  __shared__ __attribute__((aligned(1024))) char smem[4 * TILE];  // K0 V0 K1 V1
+  // PACKED tiles stream K/V that no other workgroup reads (one workgroup per
+  // KV head and tile of its rows) from HBM, where the per-head layout's K/V
+  // is shared through L2 by the q tiles and heads of one KV head. They load it
+  // non-temporally (M = 16 over cfg4's pool: +6 %, M = 8: +10 %) through three
+  // stages, each tile's DMA issued two tiles ahead (48 KB of LDS at D = 128,
+  // still three workgroups per CU; +1-2 %). The per-head layout keeps two
+  // stages: a third gained nothing there.
+  constexpr int NST = PACKED ? 3 : 2;
+  constexpr int kDmaPerTile = 2 * Slab<D, NW, BN>::IPW;  // DMA instructions per wave and tile
+  __shared__ __attribute__((aligned(1024))) char smem[2 * NST * TILE];  // K0 V0 K1 V1 (K2 V2)
   // PACKED: the q heads of the pair's KV head in head-map order, and the
   // heads whose head-map entry is outside [0, Hk) (collected by the pairs of
   // KV head 0); s_pk_n holds both counts.
@@ -835,10 +851,17 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const SlabLane<D, NW, BN> dl = slab_lane<D, NW, BN>(wave, lane);
   if (ntiles > 0) {
     const QuarterSrc s0 = pages.get(p, b, 0, kv_len, wave, lane);
-    dma_slab<D, NW, BN>(s0, dl.vk, kp, wave, smem);
-    dma_slab<D, NW, BN>(s0, dl.vv, vp, wave, smem + TILE);
+    dma_slab<D, NW, BN, PACKED>(s0, dl.vk, kp, wave, smem);
+    dma_slab<D, NW, BN, PACKED>(s0, dl.vv, vp, wave, smem + TILE);
   }
-  QuarterSrc next_src = pages.get(p, b, 1, kv_len, wave, lane);
+  if constexpr (NST == 3) {
+    if (ntiles > 1) {
+      const QuarterSrc s1 = pages.get(p, b, 1, kv_len, wave, lane);
+      dma_slab<D, NW, BN, PACKED>(s1, dl.vk, kp, wave, smem + 2 * TILE);
+      dma_slab<D, NW, BN, PACKED>(s1, dl.vv, vp, wave, smem + 3 * TILE);
+    }
+  }
+  QuarterSrc next_src = pages.get(p, b, NST - 1, kv_len, wave, lane);
 
   if (p.rope_cos != nullptr && q_ok) rope_fragment<KSTEPS, 16>(qreg, p, qo + qrow, 8 * half_id);
 
@@ -876,13 +899,24 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   auto step = [&](auto par, int t) {
     constexpr int PB = decltype(par)::value;
     const int k0 = t * BN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // this wave's DMA of tile t has landed (with three stages, tile t + 1's
+    // may still be in flight: vector loads complete in order); the barrier
+    // then makes every wave's part visible and frees the stage of tile t - 1
+    if constexpr (NST == 3) {
+      if (t + 1 < ntiles)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();
-    if (t + 1 < ntiles) {
-      char* nbuf = smem + (PB ^ 1) * 2 * TILE;
-      dma_slab<D, NW, BN>(next_src, dl.vk, kp, wave, nbuf);
-      dma_slab<D, NW, BN>(next_src, dl.vv, vp, wave, nbuf + TILE);
-      if (t + 2 < ntiles) next_src = pages.get(p, b, t + 2, kv_len, wave, lane);
+    if (t + (NST - 1) < ntiles) {
+      constexpr int NEXT = (PB + NST - 1) % NST;  // the stage tile t + NST - 1 goes to
+      char* nbuf = smem + NEXT * 2 * TILE;
+      dma_slab<D, NW, BN, PACKED>(next_src, dl.vk, kp, wave, nbuf);
+      dma_slab<D, NW, BN, PACKED>(next_src, dl.vv, vp, wave, nbuf + TILE);
+      if (t + NST < ntiles) next_src = pages.get(p, b, t + NST, kv_len, wave, lane);
     }
     if (k0 >= wave_lim_max) return;
     const char* buf = smem + PB * 2 * TILE;
@@ -963,9 +997,12 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  for (int t = 0; t < ntiles; t += 2) {
+  for (int t = 0; t < ntiles; t += NST) {
     step(std::integral_constant<int, 0>{}, t);
     if (t + 1 < ntiles) step(std::integral_constant<int, 1>{}, t + 1);
+    if constexpr (NST == 3) {
+      if (t + 2 < ntiles) step(std::integral_constant<int, 2>{}, t + 2);
+    }
   }
 
   // O leaves through LDS (128 rows x 2D bytes, the size of the two K/V
