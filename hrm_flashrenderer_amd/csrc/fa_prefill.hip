@@ -611,8 +611,9 @@ __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* vo
 
 // ---------------------------------------------------------------------------
 // Prefill on 32-key tiles: 16 KB of K and V per stage, two stages per
-// workgroup (32 KB), at most 168 VGPRs, so three workgroups (three waves per
-// SIMD) share a CU, whose waves hide each other's latency.
+// workgroup (32 KB; three, 48 KB, for packed rows), at most 168 VGPRs, so
+// three workgroups (three waves per SIMD) share a CU, whose waves hide each
+// other's latency.
 // ---------------------------------------------------------------------------
 //
 // PACKED: the 128 rows of a workgroup are (head, position) rows of one KV
