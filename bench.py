@@ -247,25 +247,50 @@ def bench_decode(w, steps, warmup, traffic_key, traffic, rotate=None, rope=None)
 
 def bench_decode_fused(w, steps, warmup, two_call, rope=None):
     """cfg4's step (append one token per sequence, then decode) as one call,
-    flash_attn_paged_append: the decode kernel takes the new token from
-    k_new / v_new and the merge kernel writes it into the pages, so the
-    append has no launch of its own. `two_call` is bench_decode's result for
-    the same workload (append kernel, then decode). GB/s counts the decode
-    bytes and the append's bytes over the fused step."""
-    nbytes = workloads.decode_bytes(w) + workloads.append_bytes(w)
+    flash_attn_paged_append in advance mode: the decode kernel takes the new
+    token from k_new / v_new and the merge kernel writes it into the pages,
+    so the append has no launch of its own. `two_call` is bench_decode's
+    result for the same workload (append kernel, then decode, at fixed
+    lengths). GB/s counts the decode bytes, with the lengths' growth, and the
+    append's bytes over the fused step."""
     stream = torch.cuda.current_stream()
+    # The decode step as the cache takes it: each call appends at seqlen[b]
+    # and advances it (the fused path), on a copy of the lengths before
+    # cfg4's append. Each call adds one key per sequence, so the lengths are
+    # reset before the warmup and before the per-launch pass, and
+    # bytes_per_step counts the timed steps' mean growth (warmup + (steps -
+    # 1) / 2 keys per sequence and KV head; a token past its sequence's mapped
+    # pages is skipped, as the append kernel skips it).
+    base = w.seqlen - 1
+    lengths = base.clone()
+    grow = warmup + (steps - 1) / 2
+    grow_bytes = grow * w.B * w.Hk * w.D * 2 * 2
+    nbytes = workloads.decode_bytes(w) + workloads.append_bytes(w) + grow_bytes
 
     def step(ev):
         if ev:
             ev[0].record(stream)
-        flash_attn_paged_append(w.q, w.k_pool, w.v_pool, w.k_new, w.v_new, w.seqlen, 16,
-                                w.head_map, False, w.append_pos if rope is not None else 0,
-                                start_pos=w.append_pos, block_table=w.block_table, rope=rope)
+        flash_attn_paged_append(w.q, w.k_pool, w.v_pool, w.k_new, w.v_new, lengths, 16,
+                                w.head_map, False, block_table=w.block_table, rope=rope)
         if ev:
             ev[1].record(stream)
 
-    wall, mean_ms = back_to_back(step, steps, warmup)
-    _, segs = timed(step, steps, 0)
+    settle(step)
+    lengths.copy_(base)
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step(None)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    mean_ms = e0.elapsed_time(e1) / steps
+    lengths.copy_(base)
+    _, segs = timed(step, steps, warmup)
     dec_ms = two_call["decode_kernel_ms_back_to_back"]
     return {
         "ms_per_step": round(wall / steps * 1e3, 4),
@@ -276,6 +301,9 @@ def bench_decode_fused(w, steps, warmup, two_call, rope=None):
         "two_call_step_ms_back_to_back": two_call["end_to_end_ms"],
         "decode_only_ms_back_to_back": dec_ms,
         "append_cost_us": round((mean_ms - dec_ms) * 1e3, 2),
+        # the decode time scaled to the grown lengths' bytes taken off instead
+        "append_cost_us_growth_corrected": round(
+            (mean_ms - dec_ms * (1 + grow_bytes / workloads.decode_bytes(w))) * 1e3, 2),
         "append_cost_us_two_call": round((two_call["end_to_end_ms"] - dec_ms) * 1e3, 2),
     }
 

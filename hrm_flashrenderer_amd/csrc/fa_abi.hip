@@ -246,7 +246,9 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
   const bool decode = decode_ok && fa::use_decode_path(B, M, Hq, Hk, heads_per_kv);
   if (app != nullptr) {
     p.app_advance = app->advance ? 1 : 0;
-    if (decode && rope_cos == nullptr && fa::fused_append_ok(B, M, Hq, Hk, heads_per_kv)) {
+    // the decode kernels take the token in advance mode, where it is every
+    // sequence's last key (its group comes last; fa_decode.hip)
+    if (decode && app->advance && fa::fused_append_ok(B, M, Hq, Hk, heads_per_kv)) {
       // the decode kernels take the new token (fa_decode.hip, APPEND)
       p.app_k = reinterpret_cast<const fa::f16*>(app->k_new);
       p.app_v = reinterpret_cast<const fa::f16*>(app->v_new);

@@ -206,6 +206,35 @@ __device__ __forceinline__ void rope_fragment(half8* q, const AttnParams& p, int
   }
 }
 
+// rope_fragment in two steps, so that the table loads can leave early: the
+// tables' rows for the fragment (c[i], s[i] for i < N/2), then the rotation
+// (ok: the position is inside the table; otherwise NaN).
+template <int N, int STRIDE>
+__device__ __forceinline__ void rope_tables(half8* c, half8* s, const AttnParams& p, int pos,
+                                            int base) {
+  constexpr int HALF = N * STRIDE / 2;
+  const bool ok = pos >= 0 && pos < p.rope_len;
+  const int64_t row = (int64_t)(ok ? pos : 0) * HALF + base;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    c[i] = *reinterpret_cast<const half8*>(p.rope_cos + row + STRIDE * i);
+    s[i] = *reinterpret_cast<const half8*>(p.rope_sin + row + STRIDE * i);
+  }
+}
+template <int N>
+__device__ __forceinline__ void rope_rotate(half8* q, const half8* c, const half8* s, bool ok) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      f16 y1, y2;
+      rope_pair(q[i][j], q[i + N / 2][j], c[i][j], s[i][j], y1, y2);
+      q[i][j] = ok ? y1 : (f16)__builtin_nanf("");
+      q[i + N / 2][j] = ok ? y2 : (f16)__builtin_nanf("");
+    }
+  }
+}
+
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, const void* v_new,
                                const KVMap& map, int B, int Hk, int T, int start_pos,
@@ -239,8 +268,8 @@ constexpr int kSegmentCost = 12;
 // kernel; needs the workspace of plan_decode) or on the prefill kernel.
 constexpr int kPackedMinTiles = 256;
 bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv);
-// Whether a paged call with a fused append (one new token per sequence, no
-// rotary tables) runs the append inside the decode kernels: the decode path
+// Whether a paged call with a fused append (one new token per sequence, at
+// position seqlen[b]) runs the append inside the decode kernels: the decode path
 // with at most two 16-row blocks of query rows per KV head (the fused
 // variants keep the new token's fragments in registers beside them).
 bool fused_append_ok(int B, int M, int Hq, int Hk, int heads_per_kv);

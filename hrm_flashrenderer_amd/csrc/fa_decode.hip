@@ -414,37 +414,20 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     const GroupLane<D> glane(n, quarter, row_bytes);
     const int g0 = g_begin + wave;
 
-    // Fused append: the group g_app of this range holding the new token (row
-    // r_app of it), or -1, and the lane's fragments of the token's K and V
-    // rows, loaded after the segment's first K/V groups and Q (they are
-    // needed only when their group comes up). The token replaces the page row
-    // only where some row sees it and where the append writes it (a mapped
-    // page, checked when the group comes up).
-    int g_app = -1, r_app = 0;
+    // Fused append (the step's new token at position seqlen[b], the
+    // sequence's last key): its group g_app is the last group of the segment
+    // and the last of the wave that owns it. That wave loads the group into
+    // app_regs, and the token's K and V rows into app_k / app_v, at the start
+    // of the pass, and processes it after the group loop with the token's row
+    // in place of the page's. So the group loop is the plain kernel's, and
+    // the group still comes last for its wave. The token replaces the page
+    // row only where some row sees it and where the append writes it (a
+    // mapped page).
+    int r_app = 0;
     u32x4 app_k[APPEND ? KSTEPS : 1];
     uint32_t app_v[APPEND ? VW : 1];
-    // The new token's row in place of the page's (group gi in ring slot r).
-    auto substitute = [&](DecodeRegs<D>& r, int gi) {
-      if constexpr (APPEND) {
-        if (gi != g_app) return;
-        // only where the append writes the token (a mapped page); the block
-        // table entry is the one the group's own loads looked up
-        if (p.kv.row_offset(b, hk, (g_app << 4) + r_app) < 0) return;
-        if (n == r_app) {
-#pragma unroll
-          for (int kk = 0; kk < KSTEPS; ++kk) r.k[kk] = app_k[kk];
-        }
-        if (quarter == (r_app >> 2)) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (i == (r_app & 3)) {
-#pragma unroll
-              for (int w2 = 0; w2 < VW; ++w2) r.v[i][w2] = app_v[w2];
-            }
-          }
-        }
-      }
-    };
+    constexpr int kAppRope = APPEND ? KSTEPS / 2 : 1;
+    half8 app_c[kAppRope], app_s[kAppRope];
     // With ALIGNED loads every prefetch is issued unconditionally (groups past
     // the end read as empty ranges), which keeps the number of loads in flight
     // the same on every path, so each group waits only for its own loads.
@@ -618,12 +601,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         }
       };
 
-      // the new token's fragments (fused append; see g_app above)
+      // the group loop's end: the new token's group (fused append) is left
+      // to its owner wave, after the loop
+      int g_loop = g_end;
+      bool app_owner = false;
+      DecodeRegs<D> app_regs;
       if constexpr (APPEND) {
         const int s = __builtin_amdgcn_readfirstlane(s_app[b]);
-        if (s >= 0 && s < t_end && (s >> 4) >= g_begin && (s >> 4) < g_end) {
-          g_app = s >> 4;
+        const bool seen = s >= 0 && s < t_end && (s >> 4) >= g_begin && (s >> 4) == g_end - 1 &&
+                          p.kv.row_offset(b, hk, s) >= 0;
+        if (seen) {
+          g_loop = s >> 4;
           r_app = s & 15;
+          app_owner = ((g_loop - g_begin) & (kDecodeWaves - 1)) == wave;
+        }
+        if (app_owner) {
+          load_group<D, ALIGNED>(app_regs, p, kp, vp, b, hk, g_loop << 4, t_end, n, quarter,
+                                 glane);
           const int64_t row = ((int64_t)b * p.Hk + hk) * D;
           // K: the lane's chunks 8*quarter + 32*kk of the row (row n of a group)
 #pragma unroll
@@ -633,23 +627,44 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.app_v + row + DPL * n);
 #pragma unroll
           for (int w2 = 0; w2 < VW; ++w2) app_v[w2] = vr[w2];
+          // chunk kk holds dims 8*quarter + 32*kk + (0..7), whose rotary
+          // partners d + D/2 are in chunk kk + KSTEPS/2 of the same lane
+          if (p.rope_cos != nullptr) rope_tables<KSTEPS, 32>(app_c, app_s, p, s, 8 * quarter);
         }
-        // wave-uniform, so that the group test and the page lookup of the
-        // substitution stay scalar
-        g_app = __builtin_amdgcn_readfirstlane(g_app);
-        r_app = __builtin_amdgcn_readfirstlane(r_app);
       }
-      for (int g = g0; g < g_end; g += RING * kDecodeWaves) {
+      for (int g = g0; g < g_loop; g += RING * kDecodeWaves) {
 #pragma unroll
         for (int i = 0; i < RING; ++i) {
           const int gi = g + i * kDecodeWaves;
-          if (gi >= g_end) break;
+          if (gi >= g_loop) break;
           const int gl = gi + (RING - 1) * kDecodeWaves;
-          if (ALIGNED || gl < g_end)
+          if (ALIGNED || gl < g_loop)
             load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
                                    quarter, glane);
-          substitute(ring[i], gi);
           process(ring[i], gi << 4);
+        }
+      }
+      if constexpr (APPEND) {
+        if (app_owner) {
+          // K rotated at the token's position, as the append kernel rotates
+          // the row it writes; then the token's row in place of the page's
+          if (p.rope_cos != nullptr)
+            rope_rotate<KSTEPS>(reinterpret_cast<half8*>(app_k), app_c, app_s,
+                                (g_loop << 4) + r_app < p.rope_len);
+          if (n == r_app) {
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) app_regs.k[kk] = app_k[kk];
+          }
+          if (quarter == (r_app >> 2)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (i == (r_app & 3)) {
+#pragma unroll
+                for (int w2 = 0; w2 < VW; ++w2) app_regs.v[i][w2] = app_v[w2];
+              }
+            }
+          }
+          process(app_regs, g_loop << 4);
         }
       }
       (void)VW;
@@ -758,7 +773,10 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
                                                     int64_t nthreads) {
   f16* kd = reinterpret_cast<f16*>(const_cast<void*>(p.k));
   f16* vd = reinterpret_cast<f16*>(const_cast<void*>(p.v));
-  constexpr int per_row = D / 8;
+  // with rotary tables a lane moves chunk c and its rotary partner c + D/16
+  // and rotates K at its position, as paged_append_rope_kernel does
+  const bool rope = p.rope_cos != nullptr;
+  const int per_row = rope ? D / 16 : D / 8;
   const int64_t total = (int64_t)p.B * p.Hk * per_row;
   for (int64_t e = first; e < total; e += nthreads) {
     const int64_t row = e / per_row;
@@ -769,10 +787,21 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
     if (pos < 0) continue;
     const int64_t dst = p.kv.row_offset(b, hk, pos);
     if (dst < 0) continue;
-    *reinterpret_cast<u32x4*>(kd + dst + 8 * c) =
-        *reinterpret_cast<const u32x4*>(p.app_k + row * D + 8 * c);
-    *reinterpret_cast<u32x4*>(vd + dst + 8 * c) =
-        *reinterpret_cast<const u32x4*>(p.app_v + row * D + 8 * c);
+    const f16* ks = p.app_k + row * D;
+    const f16* vs = p.app_v + row * D;
+    if (rope) {
+      half8 k2[2] = {*reinterpret_cast<const half8*>(ks + 8 * c),
+                     *reinterpret_cast<const half8*>(ks + 8 * c + D / 2)};
+      rope_fragment<2, D / 2>(k2, p, pos, 8 * c);
+      *reinterpret_cast<half8*>(kd + dst + 8 * c) = k2[0];
+      *reinterpret_cast<half8*>(kd + dst + 8 * c + D / 2) = k2[1];
+      *reinterpret_cast<u32x4*>(vd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(vs + 8 * c);
+      *reinterpret_cast<u32x4*>(vd + dst + 8 * c + D / 2) =
+          *reinterpret_cast<const u32x4*>(vs + 8 * c + D / 2);
+    } else {
+      *reinterpret_cast<u32x4*>(kd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(ks + 8 * c);
+      *reinterpret_cast<u32x4*>(vd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(vs + 8 * c);
+    }
   }
   if (p.app_advance) {
     int32_t* sl = const_cast<int32_t*>(p.seqlen);

@@ -372,9 +372,8 @@ class PagedKVCache:
         causal, q_offset=lengths, rope=rope)` (the reference's decode step,
         engine/llama_tp.py:183-200), but the lengths advance on the device and
         the append needs no launch of its own when the attention runs on the
-        decode kernels without rope (see flash_attn_paged_append). The query
-        rows sit at the new token's position (q_offset = the lengths before
-        the step).
+        decode kernels (see flash_attn_paged_append). The query rows sit at
+        the new token's position (q_offset = the lengths before the step).
         """
         B, Hk, T, D = k_new.shape
         if B != self.bsz or Hk != self.kv_heads or D != self.head_dim or T != 1:

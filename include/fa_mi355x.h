@@ -250,12 +250,13 @@ int fa_paged_kv_scatter(void* k_pages, void* v_pages, const void* k_new, const v
  *                 fa_flash_attn_paged_rope_fwd: K is rotated at its position
  *                 as fa_paged_kv_append_rope does, Q at q_off(b) + i.
  *   workspace : as for fa_flash_attn_paged_fwd (fa_paged_workspace_bytes).
- * When the attention runs on the decode kernels with at most 32 query rows
- * per KV head (heads_per_kv * M <= 32: single-token decode at the benchmark
- * shapes) and without rotary tables, the append costs no launch of its own:
- * the decode kernel takes the new token's row from k_new / v_new, and its
- * merge kernel, which runs after every page read, writes the row into the
- * pages (and advances seqlen). Other shapes run the append kernel, then the
+ * With advance = 1, when the attention runs on the decode kernels with at
+ * most 32 query rows per KV head (heads_per_kv * M <= 32: single-token
+ * decode at the benchmark shapes), the append costs no launch of its own:
+ * the new token is every sequence's last key, and the decode kernel takes
+ * its row from k_new / v_new (rotated there with rotary tables). The merge
+ * kernel, which runs after every page read, writes the row into the pages
+ * and advances seqlen. Other calls run the append kernel, then the
  * attention (then the advance). The results equal the two calls' as long as
  * no sequence reads a page row that another sequence's new token is written
  * to (pages shared between sequences are read-only to both). No counterpart

@@ -10,12 +10,13 @@ before the step, so a kernel that read it from the pages instead of from
 k_new / v_new would produce NaN rows. Both outputs are also held to the fp64
 oracle at the fp32-softmax bar.
 
-Shapes: 8 and 32 query rows per KV head (the fused decode kernels: one and
-two 16-row blocks), 64 rows (decode kernels with four blocks, so the append
+Shapes: 8 and 32 query rows per KV head (the fused decode kernels, in
+advance mode: one and two 16-row blocks; with explicit positions the append
+kernel runs first), 64 rows (decode kernels with four blocks, so the append
 kernel runs first) and 128-row prefill chunks (prefill path); D = 64 and 128;
-the rotary variant (append kernel first, then the rotary attention); new
-tokens at every place in a 16-key group and at page boundaries; an empty
-sequence (one key after the step).
+the rotary variant (the fused kernels rotate the new key); new tokens at
+every place in a 16-key group and at page boundaries; an empty sequence (one
+key after the step).
 """
 import pytest
 import torch
