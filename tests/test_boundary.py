@@ -366,18 +366,20 @@ def test_rope_table_validation(rope, msg):
 
 
 def _integration_shim_namespace(real: bool = False):
-    """Executes the `_ext` binding printed in INTEGRATION.md (section 3) against
-    the built library. Unless `real`, it then swaps the shim's library handle
-    for one that fails any compute call, so a test sees whether validation
-    happens first."""
-    text = open(os.path.join(REPO, "INTEGRATION.md")).read()
+    """Executes the `_ext` binding that the repository's integration guide
+    prints (its `flashattention_custom/_ext.py` block) against the built
+    library. Unless `real`, it then swaps the shim's library handle for one
+    that fails any compute call, so a test sees whether validation happens
+    first."""
+    guide = "INTEGRATION.md"
+    text = open(os.path.join(REPO, guide)).read()
     start = text.index("```python\n# flashattention_custom/_ext.py — binds")
     code = text[start + len("```python\n"):text.index("```", start + 10)]
     old = os.environ.get("FA_MI355X_LIB")
     os.environ["FA_MI355X_LIB"] = _lib.LIB_PATH
     try:
         ns = {}
-        exec(compile(code, "INTEGRATION.md:_ext.py", "exec"), ns)
+        exec(compile(code, guide + ":_ext.py", "exec"), ns)
     finally:
         if old is None:
             os.environ.pop("FA_MI355X_LIB", None)

@@ -384,7 +384,7 @@ def test_arbitrary_head_map(gpu, M):
 
 
 def test_integration_shim_rejects_bad_dtypes_and_layouts(gpu):
-    """The `_ext` binding of INTEGRATION.md on device tensors: bf16, mixed
+    """The integration guide's `_ext` binding on device tensors: bf16, mixed
     dtypes and non-contiguous inputs raise the reference's messages before
     any C call (they would otherwise reach a kernel that reads them as fp16
     or fp32); a valid call through the real library matches flash_attn."""
