@@ -16,7 +16,8 @@ kernel runs first), 64 rows (decode kernels with four blocks, so the append
 kernel runs first) and 128-row prefill chunks (prefill path); D = 64 and 128;
 the rotary variant (the fused kernels rotate the new key); new tokens at
 every place in a 16-key group and at page boundaries; an empty sequence (one
-key after the step).
+key after the step); in advance mode, a new token in an unmapped page and
+causal rows that end before the new token.
 """
 import pytest
 import torch
@@ -198,3 +199,32 @@ def test_cache_decode_steps_match_append_and_attention(gpu, rope):
             a = gather_seq(fc, fbt[b], n, 16)
             r = gather_seq(tc, tbt[b], n, 16)
             assert torch.equal(_bits(a), _bits(r)), f"sequence {b}"
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_fused_step_advance_edges(gpu, rope):
+    """Advance mode (the fused kernels) at its edges, against append +
+    attention: sequence 2's new token falls in an unmapped page (neither
+    written nor substituted; both read that key from the pool), and with
+    causal rows that end one position before the new token it is invisible
+    (written, not attended)."""
+    B, Hq, Hk, D, PS = 4, 16, 2, 128, 16
+    old = [63, 40, 63, 7]
+    kp, vp, bt, k_new, v_new, hm = _setup(B, Hq, Hk, D, PS, old, 9450)
+    ropet = build_rope_cache(256, D, device=DEV) if rope else None
+    bt[2, 3] = -1                      # position 63 of sequence 2: page 3
+    old_t = torch.tensor(old, dtype=torch.int32, device=DEV)
+    new_t = old_t + 1
+    for causal, M, qo in ((False, 1, old_t), (True, 4, torch.clamp(old_t - 4, min=0))):
+        q = seeded((B, Hq, M, D), 9451 + M)
+        kr, vr = kp.clone(), vp.clone()
+        paged_kv_append(kr, vr, k_new, v_new, old_t, PS, block_table=bt, rope=ropet)
+        o_ref = flash_attn_paged(q, kr, vr, new_t, PS, hm, causal, qo, block_table=bt, rope=ropet)
+        kf, vf, sl = kp.clone(), vp.clone(), old_t.clone()
+        o = flash_attn_paged_append(q, kf, vf, k_new, v_new, sl, PS, hm, causal, q_offset=qo,
+                                    block_table=bt, rope=ropet)
+        torch.cuda.synchronize()
+        what = f"causal={causal} M={M} rope={rope}"
+        assert torch.equal(_bits(o), _bits(o_ref)), what
+        assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr)), what
+        assert torch.equal(sl, new_t), what
