@@ -16,8 +16,9 @@ kernel runs first), 64 rows (decode kernels with four blocks, so the append
 kernel runs first) and 128-row prefill chunks (prefill path); D = 64 and 128;
 the rotary variant (the fused kernels rotate the new key); new tokens at
 every place in a 16-key group and at page boundaries; an empty sequence (one
-key after the step); in advance mode, a new token in an unmapped page and
-causal rows that end before the new token.
+key after the step); in advance mode, a new token in an unmapped page,
+causal rows that end before the new token, and pages of 24 tokens (the
+decode kernels' per-row load variant).
 """
 import pytest
 import torch
@@ -228,3 +229,26 @@ def test_fused_step_advance_edges(gpu, rope):
         assert torch.equal(_bits(o), _bits(o_ref)), what
         assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr)), what
         assert torch.equal(sl, new_t), what
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_fused_step_unaligned_pages(gpu, D):
+    """Pages of 24 tokens (not a multiple of 16: the decode kernels' per-row
+    load variant), advance mode, new tokens on both sides of page and group
+    boundaries, against append + attention."""
+    B, Hq, Hk, PS = 5, 16, 4, 24
+    old = [0, 23, 24, 47, 200]
+    kp, vp, bt, k_new, v_new, hm = _setup(B, Hq, Hk, D, PS, old, 9500 + D)
+    q = seeded((B, Hq, 1, D), 9510 + D)
+    old_t = torch.tensor(old, dtype=torch.int32, device=DEV)
+    new_t = old_t + 1
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, old_t, PS, block_table=bt)
+    o_ref = flash_attn_paged(q, kr, vr, new_t, PS, hm, False, block_table=bt)
+    kf, vf, sl = kp.clone(), vp.clone(), old_t.clone()
+    o = flash_attn_paged_append(q, kf, vf, k_new, v_new, sl, PS, hm, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref))
+    assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr))
+    assert torch.equal(sl, new_t)
+    assert not torch.isnan(o).any()
