@@ -437,11 +437,15 @@ def cpu_threads():
 def cpu_baseline_paged(w, kind, budget_s=10.0):
     """Time the oracle's restatement of the reference CPU path on this host.
 
-    The sample is a deterministic prefix of the workload's (sequence, head)
-    pairs, sequence by sequence, sized from a timed probe so that the timed
-    run takes about `budget_s`; the rate is the sample's algorithmic work (the
-    same unit as the GPU figure) over its time. Attention only: the append
-    of the decode step is a copy of B rows."""
+    The sample spreads over the workload's sequence lengths: up to
+    `n_seq` sequences at evenly spaced ranks of their key counts (shortest to
+    longest), each timed on a prefix of its q heads sized from a probe so that
+    the whole sample takes about `budget_s`. Each sampled sequence gives a
+    rate (its algorithmic work over its time); every sequence of the workload
+    is then charged its own work at the rate of the sampled sequence nearest
+    in key count, and the reported value is the whole job's work over that
+    extrapolated time (same unit as the GPU figure). Attention only: the
+    append of the decode step is a copy of B rows."""
     from oracle import attention as ora
 
     threads = cpu_threads()
@@ -461,49 +465,55 @@ def cpu_baseline_paged(w, kind, budget_s=10.0):
         off = w.q_offsets_host[b] if w.q_offsets_host else 0
         return sum(max(0, min(n, off + i + 1)) for i in range(w.M))
 
-    def run(batches, heads):
-        ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
-                                 batches=batches, heads=heads)
+    def work_of(b, nh):
+        if kind == "flops":
+            return 4.0 * w.D * pairs_of(b) * nh
+        return w.lengths[b] * w.Hk * w.D * 2 * 2 * nh / w.Hq + 2 * nh * w.M * w.D * 2
 
-    run([0], [0])                      # warm-up
+    def run(b, nh):
+        ora.cpu_flash_attn_paged(q, kp, vp, sl, 16, hm, w.causal, qo, 0, block_table=bt,
+                                 batches=[b], heads=list(range(nh)))
+
+    order = sorted(range(w.B), key=lambda b: (pairs_of(b), b))
+    n_seq = min(w.B, 4 if w.B <= 16 else 6)
+    picks = sorted({order[min(w.B - 1, int((i + 0.5) * w.B / n_seq))] for i in range(n_seq)},
+                   key=lambda b: pairs_of(b))
+    run(picks[0], 1)                   # warm-up
     t0 = time.perf_counter()
-    run([0], [0])
-    per_pair = max(time.perf_counter() - t0, 1e-5) / max(pairs_of(0), 1)
-    # a (sequence, head) costs about per_pair * pairs_of(b); take whole sequences
-    # while they fit the budget, then a prefix of the next one's heads
-    plan, spent = [], 0.0
+    run(picks[0], 1)
+    per_pair = max(time.perf_counter() - t0, 1e-5) / max(pairs_of(picks[0]), 1)
+    share = budget_s / len(picks)
+    rates, plan, spent = {}, [], 0.0
+    for b in picks:
+        nh = max(1, min(w.Hq, int(share / max(per_pair * max(pairs_of(b), 1), 1e-9))))
+        # repeated while the sequence's share of the budget lasts (at least
+        # once), so that short sequences are not timed on a few milliseconds
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            run(b, nh)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= 0.5 * share or reps >= 1000:
+                break
+        spent += dt
+        rates[b] = work_of(b, nh) * reps / max(dt, 1e-9)
+        plan.append((b, nh, reps, dt))
+    # every sequence at the rate of the sampled one nearest in key count
+    job_work, job_time = 0.0, 0.0
     for b in range(w.B):
-        head_cost = per_pair * max(pairs_of(b), 1)
-        if spent + head_cost * w.Hq <= budget_s:
-            plan.append((b, w.Hq))
-            spent += head_cost * w.Hq
-            continue
-        nh = int((budget_s - spent) / head_cost)
-        if nh >= 1:
-            plan.append((b, nh))
-        break
-    if not plan:
-        plan = [(0, 1)]
-    full = [b for b, nh in plan if nh == w.Hq]
-    part = [(b, nh) for b, nh in plan if nh < w.Hq]
-    t0 = time.perf_counter()
-    if full:
-        run(full, None)
-    for b, nh in part:
-        run([b], list(range(nh)))
-    dt = time.perf_counter() - t0
-    if kind == "flops":
-        work = sum(4.0 * w.D * pairs_of(b) * nh for b, nh in plan)
-        value, unit = work / dt / 1e12, "TFLOP/s"
-    else:
-        work = sum(w.lengths[b] * w.Hk * w.D * 2 * 2 * nh / w.Hq + 2 * nh * w.M * w.D * 2
-                   for b, nh in plan)
-        value, unit = work / dt / 1e9, "GB/s"
-    heads_done = sum(nh for _, nh in plan)
-    sample = (f"{heads_done} of {w.B * w.Hq} (sequence, head) pairs: sequences "
-              f"{plan[0][0]}..{plan[-1][0]} of {w.B}"
-              + (f" (the last with heads 0..{part[-1][1] - 1})" if part else "")
-              + f"; {dt:.2f} s on the host")
+        near = min(picks, key=lambda c: (abs(pairs_of(c) - pairs_of(b)), c))
+        wb = work_of(b, w.Hq)
+        job_work += wb
+        job_time += wb / rates[near]
+    scale = 1e12 if kind == "flops" else 1e9
+    value, unit = job_work / job_time / scale, ("TFLOP/s" if kind == "flops" else "GB/s")
+    heads_done = sum(nh for _, nh, _, _ in plan)
+    sample = (f"{heads_done} of {w.B * w.Hq} (sequence, head) pairs from {len(picks)} of {w.B} "
+              "sequences spread over the key counts ("
+              + ", ".join(f"seq {b}: {w.lengths[b]} keys, {nh} heads x {reps}, {dt:.2f} s"
+                          for b, nh, reps, dt in plan)
+              + f"); {spent:.2f} s on the host; the whole job extrapolated at each sampled "
+              "sequence's rate to the sequences nearest in key count")
     return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port",
             "sample": sample, "extrapolated": heads_done < w.B * w.Hq,
             "cpu_count": os.cpu_count(), "threads_note": "torch intra-op threads = the CPUs "

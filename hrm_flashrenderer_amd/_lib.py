@@ -14,7 +14,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 from ._build import LIB_PATH
 
-FA_ABI_VERSION = 3
+FA_ABI_VERSION = 4
 FA_DTYPE_F16 = 0
 FA_DTYPE_F32 = 1
 
@@ -26,6 +26,9 @@ _SZ = ctypes.c_size_t
 SYMBOLS = (
     ("fa_flash_attn_fwd", _I,
      [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P]),
+    ("fa_flash_attn_fwd_ws", _I,
+     [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    ("fa_flash_attn_workspace_bytes", _SZ, [_I, _I, _I, _I, _I, _I, _I]),
     ("fa_flash_attn_paged_fwd", _I,
      [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I64, _I64, _P, _P, _P, _P,
       _I, _I, _P, _SZ, _P]),

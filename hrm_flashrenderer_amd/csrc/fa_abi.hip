@@ -13,6 +13,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -124,10 +125,47 @@ int fa_abi_version(void) { return FA_ABI_VERSION; }
 
 const char* fa_last_error(void) { return g_last_error.c_str(); }
 
+// Whether a contiguous call runs on the decode kernels: fp16, at most 32
+// query rows per K/V head (the fused rows of a GQA group), and the paged
+// entry's rule for the rest.
+static bool contig_decode(int dtype, int B, int Hq, int Hk, int M, int N, int D) {
+  if (dtype != FA_DTYPE_F16 || !head_dim_ok(D) || B <= 0 || Hk <= 0 || Hq % Hk != 0 || M <= 0 ||
+      N <= 0)
+    return false;
+  const int group = Hq / Hk;
+  return (int64_t)M * group <= 32 && fa::use_decode_path(B, M, Hq, Hk, group);
+}
+
+size_t fa_flash_attn_workspace_bytes(int dtype, int B, int Hq, int Hk, int M, int N, int D) {
+  if (!contig_decode(dtype, B, Hq, Hk, M, N, D)) return 0;
+  return fa::plan_decode(B, Hq, M, D, Hk, N, Hq / Hk).ws_bytes;
+}
+
+static int contig_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                      int Hq, int Hk, int M, int N, int D, int causal, int64_t q_offset,
+                      int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
+                      void* workspace, size_t workspace_bytes, bool decode_ok, void* stream);
+
 int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
                       int Hq, int Hk, int M, int N, int D, int causal, int64_t q_offset,
                       int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
                       void* stream) {
+  return contig_fwd(q, k, v, o, dtype, B, Hq, Hk, M, N, D, causal, q_offset, k_offset, q_offsets,
+                    k_offsets, nullptr, 0, false, stream);
+}
+
+int fa_flash_attn_fwd_ws(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                         int Hq, int Hk, int M, int N, int D, int causal, int64_t q_offset,
+                         int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return contig_fwd(q, k, v, o, dtype, B, Hq, Hk, M, N, D, causal, q_offset, k_offset, q_offsets,
+                    k_offsets, workspace, workspace_bytes, true, stream);
+}
+
+static int contig_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                      int Hq, int Hk, int M, int N, int D, int causal, int64_t q_offset,
+                      int64_t k_offset, const int32_t* q_offsets, const int32_t* k_offsets,
+                      void* workspace, size_t workspace_bytes, bool decode_ok, void* stream) {
   if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_F32)
     return fail(FA_ERR_INVALID, "fp16 or fp32 required");
   if (B < 0 || Hq < 0 || Hk < 0 || M < 0 || N < 0 || D < 0)
@@ -171,6 +209,38 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int 
   p.k_offset = narrow(k_offset);
   p.scale_log2 = fa::kLog2e / sqrtf((float)D);
   (void)hipGetLastError();
+  if (decode_ok && contig_decode(dtype, B, Hq, Hk, M, N, D)) {
+    // split-K decode over the contiguous rows: one slot row per (q head of
+    // the group, query position), seqlen = N for every sequence
+    const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, N, p.group);
+    if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
+      return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    char* ws = reinterpret_cast<char*>(workspace);
+    hipError_t e = hipSuccess;
+    for (int b0 = 0; b0 < B && e == hipSuccess; b0 += fa::kDecodeMaxBatch) {
+      const int Bc = std::min(fa::kDecodeMaxBatch, B - b0);
+      fa::AttnParams pc = p;
+      const int64_t qrows = (int64_t)b0 * Hq * M * D;
+      pc.q = reinterpret_cast<const fa::f16*>(q) + qrows;
+      pc.o = reinterpret_cast<fa::f16*>(o) + qrows;
+      pc.k = reinterpret_cast<const fa::f16*>(k) + b0 * p.kv.stride_nb;
+      pc.v = reinterpret_cast<const fa::f16*>(v) + b0 * p.kv.stride_nb;
+      if (q_offsets != nullptr) pc.q_offsets = q_offsets + b0;
+      if (k_offsets != nullptr) pc.k_offsets = k_offsets + b0;
+      pc.B = Bc;
+      const fa::DecodePlan cplan = fa::plan_decode(Bc, Hq, M, D, Hk, N, p.group);
+      pc.ws_o = reinterpret_cast<float*>(ws);
+      pc.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
+      pc.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
+      pc.ws_app = pc.ws_units + (Bc + 1);
+      pc.dec_rows = cplan.rows;
+      pc.dec_seg_cost = fa::kSegmentCost;
+      pc.dec_wgs = fa::decode_launch_wgs(cplan, pc, D);
+      e = fa::launch_decode(pc, D, (hipStream_t)stream);
+    }
+    return launch_status(e);
+  }
   return launch_status(fa::launch_prefill(p, D, dtype, (hipStream_t)stream));
 }
 
@@ -276,19 +346,52 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
                                   p.rope_cos, p.rope_sin, rope_len, (hipStream_t)stream);
     }
   } else if (decode) {
+    // plan_decode sizes the workspace for one launch of at most
+    // kDecodeMaxBatch sequences; a larger batch runs in such launches one
+    // after another on the stream, each on the workspace the previous one
+    // has finished with (its combine kernel runs before the next launch).
     const fa::DecodePlan plan = fa::plan_decode(B, Hq, M, D, Hk, p.N, heads_per_kv);
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
                   workspace == nullptr ? (size_t)0 : workspace_bytes);
     char* ws = reinterpret_cast<char*>(workspace);
-    p.ws_o = reinterpret_cast<float*>(ws);
-    p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
-    p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-    p.ws_app = p.ws_units + (B + 1);
-    p.dec_wgs = fa::decode_launch_wgs(plan, p, D);
-    p.dec_seg_cost = PS % 16 == 0 ? fa::kSegmentCost : 0;
-    p.dec_rows = plan.rows;
-    e = fa::launch_decode(p, D, (hipStream_t)stream);
+    for (int b0 = 0; b0 < B && e == hipSuccess; b0 += fa::kDecodeMaxBatch) {
+      const int Bc = std::min(fa::kDecodeMaxBatch, B - b0);
+      fa::AttnParams pc = p;
+      if (b0 > 0) {
+        // the chunk's sequences: per-sequence arrays and rows from b0 on; the
+        // pool rows too when the pages are per sequence (no block table)
+        const int64_t qrows = (int64_t)b0 * Hq * M * D;
+        pc.q = reinterpret_cast<const fa::f16*>(q) + qrows;
+        pc.o = reinterpret_cast<fa::f16*>(o) + qrows;
+        pc.seqlen = seqlen + b0;
+        if (q_offsets != nullptr) pc.q_offsets = q_offsets + b0;
+        if (k_offsets != nullptr) pc.k_offsets = k_offsets + b0;
+        if (q_lens != nullptr) pc.q_lens = q_lens + b0;
+        if (block_table != nullptr) {
+          pc.kv.block_table = block_table + (int64_t)b0 * max_blocks;
+        } else {
+          pc.k = reinterpret_cast<const fa::f16*>(k_pages) + b0 * p.kv.stride_nb;
+          pc.v = reinterpret_cast<const fa::f16*>(v_pages) + b0 * p.kv.stride_nb;
+        }
+        if (pc.app_k != nullptr) {
+          pc.app_k += (int64_t)b0 * Hk * D;
+          pc.app_v += (int64_t)b0 * Hk * D;
+          if (pc.app_positions != nullptr) pc.app_positions += b0;
+        }
+      }
+      pc.B = Bc;
+      const fa::DecodePlan cplan = fa::plan_decode(Bc, Hq, M, D, Hk, p.N, heads_per_kv);
+      pc.ws_o = reinterpret_cast<float*>(ws);
+      pc.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
+      pc.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
+      pc.ws_app = pc.ws_units + (Bc + 1);
+      // every field decode_variant reads is set before the occupancy query
+      pc.dec_rows = cplan.rows;
+      pc.dec_seg_cost = PS % 16 == 0 ? fa::kSegmentCost : 0;
+      pc.dec_wgs = fa::decode_launch_wgs(cplan, pc, D);
+      e = fa::launch_decode(pc, D, (hipStream_t)stream);
+    }
   } else {
     // the prefill kernel packs the rows of a KV head's q heads (at most
     // heads_per_kv of them) into shared 128-row tiles when M < 128
@@ -509,9 +612,9 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.ws_o = reinterpret_cast<float*>(ws);
   p.ws_ml = reinterpret_cast<float*>(ws + plan.o_bytes);
   p.ws_units = reinterpret_cast<int*>(ws + plan.o_bytes + plan.ml_bytes);
-  p.dec_wgs = fa::decode_launch_wgs(plan, p, Dh);  // strided whole-group loads, fp32 query split
-  p.dec_seg_cost = 0;  // B = 1: a workgroup opens at most two segments
   p.dec_rows = plan.rows;
+  p.dec_seg_cost = 0;  // B = 1: a workgroup opens at most two segments
+  p.dec_wgs = fa::decode_launch_wgs(plan, p, Dh);  // strided whole-group loads, fp32 query split
   return launch_status(fa::launch_decode(p, Dh, (hipStream_t)stream));
 }
 

@@ -244,6 +244,11 @@ hipError_t launch_paged_append(void* k_pages, void* v_pages, const void* k_new, 
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream);
 hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream);
 
+// Sequences of one decode launch: a larger batch runs in launches of at most
+// this many consecutive sequences, one after another on the stream, which
+// share the workspace (plan_decode sizes it for one launch).
+constexpr int kDecodeMaxBatch = 2048;
+
 // Decode sizing (host side; depends on sizes only).
 struct DecodePlan {
   int wgs;          // workgroup capacity of the workspace

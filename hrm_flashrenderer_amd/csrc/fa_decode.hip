@@ -33,8 +33,6 @@
 //    workspace; a combine kernel merges the partials of a row in log2 space.
 #include "fa_common.h"
 
-#include <stdlib.h>
-
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -47,7 +45,8 @@ constexpr int kDecodeThreads = 256;  // 4 waves
 constexpr int kDecodeWaves = 4;
 constexpr int kRows = 16;            // query rows per MFMA column block
 constexpr int kMaxHeads = 256;       // q heads scanned per KV head
-constexpr int kMaxBatch = 2048;      // sequences whose unit prefix fits in LDS
+constexpr int kMaxBatch = kDecodeMaxBatch;  // sequences whose unit prefix fits in LDS
+constexpr int kDecodeMaxWgs = 1024;  // workgroup capacity of a decode workspace
 static_assert(kMaxHeads == kDecodeThreads, "the head map is read one head per thread");
 
 __device__ __forceinline__ float wave_max16x(float v) {
@@ -964,12 +963,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   }
 }
 
-int env_int(const char* name, int fallback) {
-  const char* s = getenv(name);
-  const int v = s ? atoi(s) : 0;
-  return v > 0 ? v : fallback;
-}
-
 // The decode kernel variant a call runs: row loads from whole 16-token
 // groups (ALIGNED: pages of a multiple of 16 tokens, or unpaged rows at a
 // fixed stride whose 16-row span fits a buffer range), the fp32-query split
@@ -1056,7 +1049,9 @@ int decode_grid_wgs(int D, DecodeVariant var) {
 }  // namespace
 
 bool use_decode_path(int B, int M, int Hq, int Hk, int heads_per_kv) {
-  if (Hk <= 0 || Hq > kMaxHeads || B > kMaxBatch || M < 1) return false;
+  // (a batch of more than kDecodeMaxBatch sequences runs in launches of at
+  // most that many: the unit prefix of one launch lives in LDS)
+  if (Hk <= 0 || Hq > kMaxHeads || B < 0 || M < 1) return false;
   const int64_t rows = (int64_t)M * ((Hq + Hk - 1) / Hk);  // query rows per KV head
   if (rows <= 2 * kRows) return true;
   // With M < 128 and a heads_per_kv bound, the prefill kernel packs a KV
@@ -1084,7 +1079,6 @@ bool fused_append_ok(int B, int M, int Hq, int Hk, int heads_per_kv) {
 }
 
 int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
-  if (getenv("FA_DECODE_WGS") != nullptr) return plan.wgs;
   const int r = decode_grid_wgs(D, decode_variant(p));
   return r > 0 ? std::min(plan.wgs, r) : plan.wgs;
 }
@@ -1092,12 +1086,12 @@ int decode_launch_wgs(const DecodePlan& plan, const AttnParams& p, int D) {
 DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
                        int heads_per_kv) {
   DecodePlan plan;
-  // Workspace capacity: up to 1024 workgroups (FA_DECODE_WGS overrides), but
-  // not more than the largest possible number of 16-key groups divided by 8.
-  // The launch uses min(this, one workgroup per CU).
+  B = std::min(B, kDecodeMaxBatch);  // the sequences of one launch
+  // Workspace capacity: up to kDecodeMaxWgs workgroups, but not more than the
+  // largest possible number of 16-key groups divided by 8. The launch uses
+  // min(this, one workgroup per CU).
   const int64_t max_units = (int64_t)B * Hk * ((capacity_tokens + 15) / 16);
-  int64_t wgs = env_int("FA_DECODE_WGS", 1024);
-  wgs = std::min<int64_t>(wgs, std::max<int64_t>(1, max_units / 8));
+  const int64_t wgs = std::min<int64_t>(kDecodeMaxWgs, std::max<int64_t>(1, max_units / 8));
   plan.wgs = (int)wgs;
   // a slot holds the rows of one KV head's query heads
   const int hpk = heads_per_kv <= 0 || heads_per_kv > Hq ? Hq : heads_per_kv;

@@ -132,23 +132,44 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 _HEADS_PER_KV: dict = {}
 
 
+def _count_heads_per_kv(head_map: torch.Tensor, Hk: int) -> int:
+    hm = head_map.detach().to("cpu", torch.int64).view(-1)
+    hm = hm[(hm >= 0) & (hm < Hk)]
+    n = int(torch.bincount(hm, minlength=1).max()) if hm.numel() else 0
+    return max(1, n)
+
+
 def heads_per_kv(head_map: torch.Tensor, Hk: int) -> int:
     """The most query heads `head_map` sends to one KV head (entries outside
     [0, Hk) are ignored), which sizes the decode workspace. The map is read
     back once per head-map tensor and remembered until the tensor changes or
     is freed; callers such as engine/llama_tp.py:145-156 build one map per
-    layer and reuse it on every call."""
+    layer and reuse it on every call.
+
+    A tensor made under torch.inference_mode() has no version counter, so an
+    in-place edit of it cannot be seen: its map is read back on every call.
+    Callers that know the bound pass heads_per_kv= to the operators instead
+    and skip the read-back altogether."""
+    if head_map.is_inference():
+        return _count_heads_per_kv(head_map, Hk)
     key = (id(head_map), int(Hk))
     ver = head_map._version
     hit = _HEADS_PER_KV.get(key)
     if hit is not None and hit[0]() is head_map and hit[1] == ver:
         return hit[2]
-    hm = head_map.detach().to("cpu", torch.int64).view(-1)
-    hm = hm[(hm >= 0) & (hm < Hk)]
-    n = int(torch.bincount(hm, minlength=1).max()) if hm.numel() else 0
-    n = max(1, n)
+    n = _count_heads_per_kv(head_map, Hk)
     ref = weakref.ref(head_map, lambda _r, k=key: _HEADS_PER_KV.pop(k, None))
     _HEADS_PER_KV[key] = (ref, ver, n)
+    return n
+
+
+def _resolve_heads_per_kv(given: Optional[int], head_map: torch.Tensor, Hk: int) -> int:
+    """The caller's stated bound (heads past it get NaN rows, as the kernels
+    document), or the one read from the map."""
+    if given is None:
+        return heads_per_kv(head_map, Hk)
+    n = int(given)
+    _check(n >= 1, "heads_per_kv must be >= 1")
     return n
 
 
@@ -165,11 +186,15 @@ def _flash_attn_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bo
     B, Hq, M, D = q.shape
     Hk, N = k.size(1), k.size(2)
     dtype = _lib.FA_DTYPE_F16 if q.dtype == torch.float16 else _lib.FA_DTYPE_F32
+    # few query rows per K/V head (decode over a contiguous cache) take the
+    # split-K decode kernels, which need a workspace
+    ws_bytes = lib.fa_flash_attn_workspace_bytes(dtype, B, Hq, Hk, M, N, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with _DeviceScope(q) as stream:
-        _lib.check(lib.fa_flash_attn_fwd(
+        _lib.check(lib.fa_flash_attn_fwd_ws(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
             B, Hq, Hk, M, N, D, int(causal), q_offset, k_offset,
-            _ptr(q_offsets), _ptr(k_offsets), stream))
+            _ptr(q_offsets), _ptr(k_offsets), _ptr(ws), ws_bytes, stream))
     return o
 
 
@@ -376,7 +401,7 @@ def validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
 
 def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
                      causal=True, q_offset=0, k_offset=0, *, block_table=None, rope=None,
-                     q_lens=None):
+                     q_lens=None, heads_per_kv=None):
     """Attention of q over paged K/V (prefill chunk or decode).
 
     Reference: flashattention_custom/ops.py:85-92 -> csrc/ext.cpp:42-68.
@@ -387,6 +412,9 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
     With q_lens (int32 device tensor [B]), only rows i < q_lens[b] of
     sequence b are live (a ragged chunk padded to M rows): the others are not
     computed and come out as zeros.
+    heads_per_kv: the most q heads head_map sends to one KV head, when the
+    caller knows it (skips reading the map back to the host; heads past a
+    stated bound come out as NaN rows).
     """
     page_size = int(page_size)
     validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
@@ -404,7 +432,7 @@ def flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map,
         _check(q_lens.dtype == torch.int32, "q_lens int32 required")
         _check(q_lens.is_contiguous(), "contiguous required")
         _check(q_lens.dim() == 1 and q_lens.numel() == B, "q_lens [B] required")
-    hpk = heads_per_kv(head_map, k_pages.size(1))
+    hpk = _resolve_heads_per_kv(heads_per_kv, head_map, k_pages.size(1))
     return _flash_attn_paged_op(q, k_pages, v_pages, seqlen, page_size, head_map, bool(causal),
                                 qo, ko, qo_t, ko_t, block_table, cos, sin, q_lens, hpk)
 
@@ -468,7 +496,7 @@ def paged_kv_append(k_pages, v_pages, k_new, v_new, start_pos, page_size, *, blo
 
 def flash_attn_paged_append(q, k_pages, v_pages, k_new, v_new, seqlen, page_size, head_map,
                             causal=False, q_offset=None, *, start_pos=None, block_table=None,
-                            rope=None):
+                            rope=None, heads_per_kv=None):
     """One decode step in one call: `paged_kv_append` of one new token per
     sequence, then `flash_attn_paged` over the pages that now hold it; returns
     the attention output shaped like q.
@@ -493,6 +521,7 @@ def flash_attn_paged_append(q, k_pages, v_pages, k_new, v_new, seqlen, page_size
         already counts it; q_offset defaults to 0, as in flash_attn_paged.
     rope=(cos, sin): K is rotated at its position as paged_kv_append(rope=)
         does, and q at q_offset + i as flash_attn_paged(rope=) does.
+    heads_per_kv: as in flash_attn_paged.
     """
     page_size = int(page_size)
     validate_flash_attn_paged(q, k_pages, v_pages, seqlen, page_size, head_map, block_table)
@@ -516,7 +545,7 @@ def flash_attn_paged_append(q, k_pages, v_pages, k_new, v_new, seqlen, page_size
             _check(qo >= 0 and qo + q.size(2) <= cos.size(0),
                    f"positions {qo}..{qo + q.size(2) - 1} are outside the rotary table "
                    f"of {cos.size(0)}")
-    hpk = heads_per_kv(head_map, k_pages.size(1))
+    hpk = _resolve_heads_per_kv(heads_per_kv, head_map, k_pages.size(1))
     return _flash_attn_paged_append_op(q, k_pages, v_pages, seqlen, page_size, head_map,
                                        bool(causal), qo, qo_t, block_table, k_new, v_new,
                                        advance, sp, sp_t, cos, sin, hpk)

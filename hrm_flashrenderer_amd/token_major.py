@@ -22,7 +22,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .ops import _DeviceScope, _check, heads_per_kv
+from .ops import _DeviceScope, _check, _resolve_heads_per_kv
 
 
 def workspace_bytes(heads: int, kv_heads: int, head_dim: int, t_max: int,
@@ -37,7 +37,8 @@ def workspace_bytes(heads: int, kv_heads: int, head_dim: int, t_max: int,
 
 def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, t: int,
                        *, scale: Optional[float] = None, head_map: Optional[torch.Tensor] = None,
-                       workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       workspace: Optional[torch.Tensor] = None,
+                       heads_per_kv: Optional[int] = None) -> torch.Tensor:
     """One decode step of attn_decode (deepseek_native_engine.sh:562-604).
 
     q: fp32 [H, Dh]; k_cache, v_cache: fp16 [T, KVH, Dh] (the engine's
@@ -45,6 +46,8 @@ def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
     scale: default 1/sqrt(Dh), the engine's inv_sqrt_dh (:1077).
     head_map: optional int32 [H]; default h % KVH, the engine's mapping (:568).
     workspace: optional uint8 device tensor of at least workspace_bytes(...).
+    heads_per_kv: with a head_map, the most heads it sends to one KV head
+    when the caller knows it (otherwise the map is read back once per map).
     Returns fp32 [H, Dh].
     """
     _check(q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "q/k/v must be CUDA")
@@ -67,7 +70,7 @@ def decode_token_major(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
         _check(head_map.is_contiguous() and head_map.numel() == H, "head_map [H] required")
     sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
     lib = _lib.load()
-    hpk = -(-H // KVH) if head_map is None else heads_per_kv(head_map, KVH)
+    hpk = -(-H // KVH) if head_map is None else _resolve_heads_per_kv(heads_per_kv, head_map, KVH)
     need = lib.fa_decode_token_major_workspace_bytes(H, KVH, Dh, t, hpk)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)

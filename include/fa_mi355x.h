@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 /* element type of q / k / v / o */
 #define FA_DTYPE_F16 0
@@ -67,6 +67,31 @@ int fa_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
                       int causal, int64_t q_offset, int64_t k_offset,
                       const int32_t* q_offsets, const int32_t* k_offsets,
                       void* stream);
+
+/*
+ * fa_flash_attn_fwd with a workspace, so that calls with few query rows run
+ * on the split-K decode kernels. The reference serves every M with one
+ * launcher, grid (B, H, ceil(M/16)) (csrc/flash_attn_sm75.cu:428-467); here
+ * fp16 calls with at most 32 query rows per K/V head (M * Hq/Hk <= 32, e.g.
+ * single-token decode over a contiguous cache) split each K/V head's keys
+ * over the whole device and merge the partial results in a second kernel,
+ * while other calls take the prefill kernels exactly as fa_flash_attn_fwd
+ * does. Arguments and results are fa_flash_attn_fwd's.
+ *   workspace : device scratch of at least fa_flash_attn_workspace_bytes(...)
+ *               bytes for the same sizes (may be NULL when that is 0); its
+ *               contents need no initialisation.
+ */
+int fa_flash_attn_fwd_ws(const void* q, const void* k, const void* v, void* o,
+                         int dtype, int B, int Hq, int Hk, int M, int N, int D,
+                         int causal, int64_t q_offset, int64_t k_offset,
+                         const int32_t* q_offsets, const int32_t* k_offsets,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes fa_flash_attn_fwd_ws needs for these sizes (0: the call
+ * runs on the prefill kernels and needs none). Host-known sizes only.
+ */
+size_t fa_flash_attn_workspace_bytes(int dtype, int B, int Hq, int Hk, int M, int N, int D);
 
 /*
  * Paged attention over a K/V page pool (prefill chunk or single-token decode).
@@ -146,7 +171,9 @@ int fa_flash_attn_paged_fwd_noalloc(const void* q, const void* k_pages, const vo
  * heads_per_kv bound. It depends only on host-known sizes (the per-sequence
  * capacity in pages is P, or max_blocks when a block table is used), never on
  * device contents: (B*Hk + W) slots x heads_per_kv*M rows x (D + 2) fp32, W
- * the decode workgroup count (<= 1024), plus 2*B + 1 ints.
+ * the decode workgroup count (<= 1024), plus 2*B + 1 ints, with B capped at
+ * 2048: a larger batch runs in decode launches of at most 2048 sequences one
+ * after another, which share the workspace.
  */
 size_t fa_paged_workspace_bytes(int B, int Hq, int M, int D, int Hk,
                                 int capacity_pages, int page_size, int heads_per_kv);

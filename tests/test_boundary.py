@@ -31,7 +31,8 @@ def declared_functions():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "fa_abi_version", "fa_decode_token_major", "fa_decode_token_major_workspace_bytes",
-        "fa_flash_attn_fwd", "fa_flash_attn_paged_append_fwd", "fa_flash_attn_paged_fwd",
+        "fa_flash_attn_fwd", "fa_flash_attn_fwd_ws", "fa_flash_attn_workspace_bytes",
+        "fa_flash_attn_paged_append_fwd", "fa_flash_attn_paged_fwd",
         "fa_flash_attn_paged_fwd_noalloc",
         "fa_flash_attn_paged_rope_fwd", "fa_last_error", "fa_paged_kv_append",
         "fa_paged_kv_append_rope", "fa_paged_kv_scatter", "fa_paged_workspace_bytes"])
@@ -187,6 +188,31 @@ def test_workspace_sizing_depends_on_sizes_only():
     assert ws0 == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 3 * 4
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100, 5) < ws
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max, 5) == 0
+    # a batch beyond 2048 sequences: decode launches of at most 2048, one
+    # workspace sized for one of them
+    big = lib.fa_paged_workspace_bytes(5000, 8, 1, 64, 2, 64, 16, 4)
+    assert big == lib.fa_paged_workspace_bytes(2048, 8, 1, 64, 2, 64, 16, 4) > 0
+
+
+def test_contiguous_workspace_sizing():
+    """fa_flash_attn_workspace_bytes: fp16 calls with at most 32 query rows
+    per K/V head take the decode kernels (workspace as for the paged entry
+    with heads_per_kv = Hq/Hk and the key count N as the capacity); fp32,
+    more rows, N == 0 or an unsupported head_dim need none."""
+    lib = _lib.load()
+    F16, F32 = _lib.FA_DTYPE_F16, _lib.FA_DTYPE_F32
+    ws = lib.fa_flash_attn_workspace_bytes(F16, 4, 40, 8, 1, 4096, 128)
+    assert ws == lib.fa_paged_workspace_bytes(4, 40, 1, 128, 8, 256, 16, 5) > 0
+    assert lib.fa_flash_attn_workspace_bytes(F16, 2, 8, 8, 4, 300, 64) > 0    # MHA, M = 4
+    assert lib.fa_flash_attn_workspace_bytes(F16, 2, 8, 8, 33, 300, 64) == 0  # 33 rows
+    assert lib.fa_flash_attn_workspace_bytes(F16, 1, 64, 8, 8, 300, 128) == 0  # 64 rows
+    assert lib.fa_flash_attn_workspace_bytes(F32, 4, 40, 8, 1, 4096, 128) == 0
+    assert lib.fa_flash_attn_workspace_bytes(F16, 4, 40, 8, 1, 0, 128) == 0
+    assert lib.fa_flash_attn_workspace_bytes(F16, 4, 40, 8, 1, 64, 96) == 0
+    P = ctypes.c_void_p(16)  # never dereferenced: the workspace check comes first
+    rc, msg = _status_and_message(lib.fa_flash_attn_fwd_ws(
+        P, P, P, P, F16, 4, 40, 8, 1, 4096, 128, 0, 0, 0, None, None, None, 0, None))
+    assert rc == -3 and msg.startswith("workspace of"), msg
 
 
 def test_heads_per_kv_of_a_head_map():
@@ -200,6 +226,48 @@ def test_heads_per_kv_of_a_head_map():
     hm2[0] = 1                              # in-place change: read again
     assert heads_per_kv(hm2, 3) == 2
     assert heads_per_kv(torch.tensor([5, -1, 7], dtype=torch.int32), 3) == 1  # invalid entries
+
+
+def test_heads_per_kv_of_an_inference_tensor():
+    """A head map made under torch.inference_mode() has no version counter:
+    the bound is read from it on every call (an in-place edit inside
+    inference mode is seen), and no RuntimeError escapes."""
+    from hrm_flashrenderer_amd.ops import heads_per_kv
+    with torch.inference_mode():
+        hm = torch.tensor([2, 0, 2, 1, 2, 0], dtype=torch.int32)
+        assert hm.is_inference()
+        assert heads_per_kv(hm, 3) == 3
+        hm[0] = 1
+        assert heads_per_kv(hm, 3) == 2
+    assert heads_per_kv(hm, 3) == 2  # outside inference mode too
+
+
+def test_stated_heads_per_kv_skips_the_map():
+    """heads_per_kv= on the operators: a stated bound is used as given (no
+    read-back) and must be at least 1."""
+    from hrm_flashrenderer_amd.ops import _resolve_heads_per_kv
+    hm = torch.tensor([0, 0, 0, 1], dtype=torch.int32)
+    assert _resolve_heads_per_kv(None, hm, 2) == 3
+    assert _resolve_heads_per_kv(5, hm, 2) == 5
+    with pytest.raises(RuntimeError, match="heads_per_kv must be >= 1"):
+        _resolve_heads_per_kv(0, hm, 2)
+    for fn in (ops.flash_attn_paged, ops.flash_attn_paged_append):
+        p = inspect.signature(fn).parameters["heads_per_kv"]
+        assert p.kind is inspect.Parameter.KEYWORD_ONLY and p.default is None
+
+
+def test_no_alloc_entry_rejects_shapes_beyond_its_scratch():
+    """fa_flash_attn_paged_fwd_noalloc refuses a decode call whose partial
+    results exceed its 32 MiB static scratch, before anything touches a device
+    (the pointers are never dereferenced)."""
+    lib = _lib.load()
+    P = ctypes.c_void_p(16)
+    need = lib.fa_paged_workspace_bytes(2048, 64, 1, 128, 8, 2049, 16, 8)
+    assert need > 32 << 20
+    rc = lib.fa_flash_attn_paged_fwd_noalloc(P, P, P, P, 16, P, P, 2048, 64, 1, 128, 1, 8, 40000,
+                                              0, 0, 0, None, None, None, P, 2049, 8, None)
+    msg = lib.fa_last_error().decode()
+    assert rc == -3 and "allocation-free entry holds 33554432" in msg, msg
 
 
 def test_signatures_match_reference():

@@ -84,6 +84,37 @@ def test_append_full_size_decode_step(gpu):
     assert torch.equal(torch.where(keep, w.v_pool, 0), torch.where(keep, v_before, 0))
 
 
+def test_append_golden_reference_vectors(gpu):
+    """The HIP kernel on the reference CPU path's own append vectors
+    (tests/golden/ref_cpu_path.npz, written by flashattention_custom/ops.py:
+    63-72 from these inputs): every page of both pools bit for bit."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_cpu_path.npz"),
+                allow_pickle=False)
+    start, ps = g["append/meta"].tolist()
+    kp = torch.from_numpy(g["append/k_pages_in"]).to(gpu)
+    vp = torch.from_numpy(g["append/v_pages_in"]).to(gpu)
+    kn = torch.from_numpy(g["append/k_new"]).to(gpu)
+    vn = torch.from_numpy(g["append/v_new"]).to(gpu)
+    paged_kv_append(kp, vp, kn, vn, start, ps)
+    torch.cuda.synchronize()
+    assert _bitexact(kp, g["append/k_pages_out"]) and _bitexact(vp, g["append/v_pages_out"])
+    # the same write with a per-sequence start tensor and an identity block table
+    B, Hk, P = g["append/k_pages_in"].shape[:3]
+    kp2 = torch.from_numpy(g["append/k_pages_in"]).to(gpu).reshape(1, B, Hk, P, ps, -1)
+    kp2 = kp2.permute(0, 2, 1, 3, 4, 5).reshape(1, Hk, B * P, ps, -1).contiguous()
+    vp2 = torch.from_numpy(g["append/v_pages_in"]).to(gpu).reshape(1, B, Hk, P, ps, -1)
+    vp2 = vp2.permute(0, 2, 1, 3, 4, 5).reshape(1, Hk, B * P, ps, -1).contiguous()
+    bt = torch.arange(B * P, dtype=torch.int32, device=gpu).view(B, P)
+    starts = torch.full((B,), start, dtype=torch.int32, device=gpu)
+    paged_kv_append(kp2, vp2, kn, vn, starts, ps, block_table=bt)
+    torch.cuda.synchronize()
+    back = lambda t: t.view(1, Hk, B, P, ps, -1).permute(0, 2, 1, 3, 4, 5).reshape(  # noqa: E731
+        B, Hk, P, ps, -1)
+    assert _bitexact(back(kp2), g["append/k_pages_out"])
+    assert _bitexact(back(vp2), g["append/v_pages_out"])
+
+
 def test_append_rejects_out_of_range_scalar_start(gpu):
     kp = torch.zeros(1, 1, 2, 16, 64, dtype=torch.float16, device=gpu)
     kn = torch.zeros(1, 1, 4, 64, dtype=torch.float16, device=gpu)

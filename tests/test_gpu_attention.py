@@ -111,6 +111,163 @@ def test_contiguous_gqa_offsets_noncausal(gpu, dtype, D):
           "per-sequence q_offset")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hk,M,N,causal,qo", [
+    (40, 8, 1, 4097, False, 0),    # single-token decode, GQA 5 rows per K/V head
+    (64, 8, 1, 1000, True, 999),   # causal decode at the last position
+    (40, 8, 4, 777, True, 773),    # 4 positions x 5 heads = 20 rows per K/V head
+    (8, 8, 4, 37, False, 0),       # MHA, short
+    (8, 8, 2, 300, True, 150),     # rows that see part of the keys
+])
+def test_contiguous_decode_rows(gpu, D, Hq, Hk, M, N, causal, qo):
+    """flash_attn with at most 32 query rows per K/V head runs on the split-K
+    decode kernels (the call asks for a workspace); same bar against fp64."""
+    from hrm_flashrenderer_amd import _lib
+    B = 3
+    lib = _lib.load()
+    assert lib.fa_flash_attn_workspace_bytes(_lib.FA_DTYPE_F16, B, Hq, Hk, M, N, D) > 0
+    q, k, v = seeded((B, Hq, M, D), 60 + M), seeded((B, Hk, N, D), 61), seeded((B, Hk, N, D), 62)
+    out = flash_attn(q, k, v, causal, qo, 0).cpu()
+    assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal, qo, 0),
+                 f"D={D} {Hq}/{Hk} M={M} N={N}")
+    qo_t = torch.tensor([qo, max(qo - 5, 0), 3], dtype=torch.int32, device=gpu)
+    out = flash_attn(q, k, v, True, qo_t, 0).cpu()
+    assert_close(out, ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), True, qo_t.tolist(), 0),
+                 "per-sequence q_offset")
+
+
+def test_contiguous_decode_matches_prefill_kernel(gpu):
+    """The same single-token calls through fa_flash_attn_fwd (prefill kernels,
+    no workspace) and fa_flash_attn_fwd_ws (decode kernels): both within the
+    bar of each other's fp64 reference and of each other."""
+    from hrm_flashrenderer_amd import _lib
+    lib = _lib.load()
+    B, Hq, Hk, M, N, D = 4, 64, 8, 1, 2500, 128
+    q, k, v = seeded((B, Hq, M, D), 70), seeded((B, Hk, N, D), 71), seeded((B, Hk, N, D), 72)
+    o_pre, o_dec = torch.empty_like(q), torch.empty_like(q)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.fa_flash_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o_pre.data_ptr(),
+                                     0, B, Hq, Hk, M, N, D, 0, 0, 0, None, None, stream))
+    nbytes = lib.fa_flash_attn_workspace_bytes(0, B, Hq, Hk, M, N, D)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    _lib.check(lib.fa_flash_attn_fwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                        o_dec.data_ptr(), 0, B, Hq, Hk, M, N, D, 0, 0, 0, None,
+                                        None, ws.data_ptr(), nbytes, stream))
+    torch.cuda.synchronize()
+    ref = ora.attention_f64(q.cpu(), k.cpu(), v.cpu(), False)
+    assert_close(o_pre.cpu(), ref, "prefill kernels")
+    assert_close(o_dec.cpu(), ref, "decode kernels")
+
+
+def _many_sequences(B, Hq, Hk, D, lengths, seed, per_sequence=False, PS=16):
+    g = torch.Generator().manual_seed(seed)
+    pages = [(n + PS - 1) // PS for n in lengths]
+    mb = max(pages) + 1
+    if per_sequence:
+        bt = torch.arange(B * mb, dtype=torch.int32).view(B, mb)
+        NB, P = B, mb
+    else:
+        total = sum(pages) + 7
+        perm = torch.randperm(total, generator=g).to(torch.int32)
+        bt = torch.full((B, mb), -1, dtype=torch.int32)
+        pos = 0
+        for b, n in enumerate(pages):
+            bt[b, :n] = perm[pos:pos + n]
+            pos += n
+        NB, P = 1, total
+    kp, vp = seeded((NB, Hk, P, PS, D), seed + 1), seeded((NB, Hk, P, PS, D), seed + 2)
+    poison_dead_slots(kp, vp, bt, lengths, PS)
+    return kp, vp, bt
+
+
+def _decode_rows_reference(q, kp, vp, bt, lengths, hm, PS=16):
+    from paged_ref import gather_seq
+    qc, kc, vc, hmc = q.cpu(), kp.cpu(), vp.cpu(), hm.cpu()
+    out = np.zeros(tuple(q.shape))
+    for b, n in enumerate(lengths):
+        ks, vs = gather_seq(kc, bt[b], n, PS), gather_seq(vc, bt[b], n, PS)
+        out[b] = ora.attention_f64(qc[b:b + 1], ks[None], vs[None], False, head_map=hmc)[0]
+    return out
+
+
+@pytest.mark.parametrize("per_sequence", [False, True])
+def test_decode_batch_beyond_2048_sequences(gpu, per_sequence):
+    """2100 sequences (more than one decode launch holds): the decode kernels
+    run in launches of at most 2048 sequences; every row against fp64, over a
+    shared permuted pool (block table) and over per-sequence pool rows (the
+    reference's [B, Hk, P, PS, D] layout, no block table)."""
+    B, Hq, Hk, D = 2100, 8, 2, 64
+    g = torch.Generator().manual_seed(77)
+    lengths = torch.randint(1, 81, (B,), generator=g).tolist()
+    kp, vp, bt = _many_sequences(B, Hq, Hk, D, lengths, 7700, per_sequence)
+    q = seeded((B, Hq, 1, D), 7710)
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    seqlen = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    out = flash_attn_paged(q, kp, vp, seqlen, 16, hm, False,
+                           block_table=None if per_sequence else bt.to(gpu))
+    ref = _decode_rows_reference(q, kp, vp, bt, lengths, hm)
+    assert_close(out.cpu().numpy(), ref, f"B={B} per_sequence={per_sequence}")
+
+
+def test_fused_decode_step_beyond_2048_sequences(gpu):
+    """The fused decode step (advance mode) over 2100 sequences: output, pages
+    and lengths bit for bit those of append + attention."""
+    from hrm_flashrenderer_amd import flash_attn_paged_append
+    B, Hq, Hk, D = 2100, 8, 2, 64
+    g = torch.Generator().manual_seed(78)
+    old = torch.randint(0, 64, (B,), generator=g).tolist()
+    kp, vp, bt = _many_sequences(B, Hq, Hk, D, [n + 1 for n in old], 7800)
+    poison_dead_slots(kp, vp, bt, old, 16)
+    bt = bt.to(gpu)
+    q = seeded((B, Hq, 1, D), 7810)
+    k_new, v_new = seeded((B, Hk, 1, D), 7811), seeded((B, Hk, 1, D), 7812)
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    old_t = torch.tensor(old, dtype=torch.int32, device=gpu)
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, old_t, 16, block_table=bt)
+    o_ref = flash_attn_paged(q, kr, vr, old_t + 1, 16, hm, False, block_table=bt)
+    sl = old_t.clone()
+    o = flash_attn_paged_append(q, kp, vp, k_new, v_new, sl, 16, hm, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(kp.view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(vp.view(torch.int16), vr.view(torch.int16))
+    assert torch.equal(sl, old_t + 1)
+    assert not torch.isnan(o).any()
+
+
+def test_operators_under_inference_mode(gpu):
+    """Head maps, pages and queries made under torch.inference_mode() (no
+    version counters): the paged operators, the fused step and a stated
+    heads_per_kv give the results of the same calls outside it."""
+    from hrm_flashrenderer_amd import flash_attn_paged_append
+    B, Hq, Hk, D = 3, 16, 4, 128
+    lengths = [50, 300, 17]
+    kp, vp, bt = _many_sequences(B, Hq, Hk, D, [n + 1 for n in lengths], 7900)
+    q = seeded((B, Hq, 1, D), 7910)
+    hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+    seqlen = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    bt = bt.to(gpu)
+    ref = flash_attn_paged(q, kp, vp, seqlen, 16, hm, False, block_table=bt)
+    with torch.inference_mode():
+        hm_i = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
+        assert hm_i.is_inference()
+        out = flash_attn_paged(q, kp, vp, seqlen, 16, hm_i, False, block_table=bt)
+        out_b = flash_attn_paged(q, kp, vp, seqlen, 16, hm_i, False, block_table=bt,
+                                 heads_per_kv=Hq // Hk)
+        k_i, v_i, sl_i = kp.clone(), vp.clone(), seqlen.clone()
+        k_new, v_new = seeded((B, Hk, 1, D), 7920), seeded((B, Hk, 1, D), 7921)
+        o_f = flash_attn_paged_append(q, k_i, v_i, k_new, v_new, sl_i, 16, hm_i, block_table=bt)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref) and torch.equal(out_b, ref)
+    kr, vr = kp.clone(), vp.clone()
+    paged_kv_append(kr, vr, k_new, v_new, seqlen, 16, block_table=bt)
+    o_r = flash_attn_paged(q, kr, vr, seqlen + 1, 16, hm, False, block_table=bt)
+    assert torch.equal(o_f, o_r) and torch.equal(sl_i, seqlen + 1)
+    assert torch.equal(k_i.view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(v_i.view(torch.int16), vr.view(torch.int16))
+
+
 # ----------------------------------------------------------- paged path ----
 
 def _small_paged(B, Hq, Hk, M, lengths, PS=16, D=128, seed=0, causal=True, q_offsets=None,

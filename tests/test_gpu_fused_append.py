@@ -252,3 +252,57 @@ def test_fused_step_unaligned_pages(gpu, D):
     assert torch.equal(_bits(kf), _bits(kr)) and torch.equal(_bits(vf), _bits(vr))
     assert torch.equal(sl, new_t)
     assert not torch.isnan(o).any()
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_full_size_cfg4_fused_step(gpu, rope):
+    """cfg4 at full size (B = 64, 64/8 heads, D = 128, contexts U[1024, 16384]
+    over the permuted shared pool) as one fused step in advance mode, the call
+    PagedKVCache.decode_step makes and the bench times. Output, both pools (as
+    raw bits, NaN-poisoned dead slots and the new token's NaN slot included)
+    and the lengths equal append + attention; every output row is held to
+    the fp64 oracle. With rope, the oracle rotates q (at the new token's
+    position) and the new key with the fp16 apply_rope restatement, and
+    attends over the unrotated cached keys plus that rotated key."""
+    import numpy as np
+
+    from hrm_flashrenderer_amd import workloads
+    from oracle import attention as ora
+    from paged_ref import decode_reference
+
+    w = workloads.cfg4(DEV)
+    old = [n - 1 for n in w.lengths]            # contexts before the step
+    bt = w.block_table
+    poison_dead_slots(w.k_pool, w.v_pool, bt, old, 16)
+    old_t = torch.tensor(old, dtype=torch.int32, device=DEV)
+    ropet = None
+    if rope:
+        cos, sin = ora.rope_tables(16385, 128)
+        ropet = (torch.from_numpy(cos).to(DEV), torch.from_numpy(sin).to(DEV))
+    kr, vr = w.k_pool.clone(), w.v_pool.clone()
+    paged_kv_append(kr, vr, w.k_new, w.v_new, old_t, 16, block_table=bt, rope=ropet)
+    o_ref = flash_attn_paged(w.q, kr, vr, old_t + 1, 16, w.head_map, False, old_t,
+                             block_table=bt, rope=ropet)
+    sl = old_t.clone()
+    o = flash_attn_paged_append(w.q, w.k_pool, w.v_pool, w.k_new, w.v_new, sl, 16, w.head_map,
+                                block_table=bt, rope=ropet)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o), _bits(o_ref)), "output differs from append + attention"
+    assert torch.equal(_bits(w.k_pool), _bits(kr)) and torch.equal(_bits(w.v_pool), _bits(vr))
+    assert torch.equal(sl, old_t + 1)
+    assert not torch.isnan(o).any()
+    del kr, vr
+    if rope:
+        # the oracle's rotation of q and of the new key (the pool's other keys
+        # are cached as they are), written into a host copy of the pool
+        qc = ora.rope_f16(w.q.cpu(), cos, sin, np.array(old)[:, None, None])
+        kn = ora.rope_f16(w.k_new.cpu(), cos, sin, np.array(old)[:, None, None])
+        w.q = torch.from_numpy(qc)
+        kpool = w.k_pool.cpu()
+        btc = bt.cpu()
+        for b, s in enumerate(old):
+            phi = int(btc[b, s // 16])
+            kpool[0, :, phi, s % 16] = torch.from_numpy(kn[b, :, 0])
+        w.k_pool = kpool
+    ref = decode_reference(w)
+    assert_close(o.cpu().numpy(), ref, f"cfg4 fused step rope={rope}")

@@ -3,11 +3,10 @@ through the C ABI: its outputs must equal fa_flash_attn_paged_fwd's (same
 kernels; the decode partials live in the library's static scratch instead of
 a caller workspace) on two calls in a row, the second smaller than the first
 (the scratch keeps the first call's contents), on a prefill call (no
-scratch), and with a per-call stream; more than 64 rows per KV head beyond
-the scratch run on the prefill kernel, other shapes whose workspace exceeds
-the scratch are rejected before any launch."""
-import ctypes
-
+scratch), and on a second stream ordered after the first by an event. More
+than 64 rows per KV head beyond the scratch run on the prefill kernel. (The
+rejection of other shapes beyond the scratch needs no device and is tested in
+test_boundary.py.)"""
 import pytest
 import torch
 
@@ -49,9 +48,9 @@ def _args(c, o):
              c["bt"].size(1)), hpk, (B, Hq, M, D, Hk, c["bt"].size(1), c["PS"]))
 
 
-def _both(c):
+def _both(c, stream=None):
     lib = _lib.load()
-    stream = torch.cuda.current_stream().cuda_stream
+    stream = (stream or torch.cuda.current_stream()).cuda_stream
     o_ref, o_new = torch.empty_like(c["q"]), torch.empty_like(c["q"])
     a_ref, hpk, shape = _args(c, o_ref)
     ws_bytes = lib.fa_paged_workspace_bytes(*shape, hpk)
@@ -82,6 +81,22 @@ def test_no_alloc_entry_matches_the_workspace_entry(gpu):
         assert torch.isfinite(new).all(), name
 
 
+def test_no_alloc_entry_on_a_second_stream(gpu):
+    """Both entries launched on a second stream (default priority) that waits
+    for the inputs made on the current stream, with the current stream
+    waiting for the second one's results: the same outputs, bit for bit."""
+    g = torch.Generator().manual_seed(960)
+    c = _case(9, 32, 8, 1, torch.randint(100, 5000, (9,), generator=g).tolist(), 961, False)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ref, new, ws_bytes = _both(c, side)
+    torch.cuda.current_stream().wait_stream(side)
+    assert ws_bytes > 0
+    assert _same(ref, new)
+    assert torch.isfinite(new).all()
+
+
 def test_no_alloc_entry_runs_many_rows_on_the_prefill_kernel(gpu):
     """256 query rows per KV head over two sequences: the workspace entry runs
     the decode kernels in four passes (its workspace is beyond the 32 MiB
@@ -93,14 +108,3 @@ def test_no_alloc_entry_runs_many_rows_on_the_prefill_kernel(gpu):
     assert ws_bytes > 32 << 20
     assert torch.isfinite(new).all()
     assert_close(new.numpy(), ref.double().numpy(), "no-alloc prefill vs decode passes")
-
-
-def test_no_alloc_entry_rejects_shapes_beyond_its_scratch(gpu):
-    lib = _lib.load()
-    P = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
-    need = lib.fa_paged_workspace_bytes(2048, 64, 1, 128, 8, 2049, 16, 8)
-    assert need > 32 << 20
-    rc = lib.fa_flash_attn_paged_fwd_noalloc(P, P, P, P, 16, P, P, 2048, 64, 1, 128, 1, 8, 40000,
-                                              0, 0, 0, None, None, None, P, 2049, 8, None)
-    msg = lib.fa_last_error().decode()
-    assert rc == -3 and "allocation-free entry holds 33554432" in msg, msg
