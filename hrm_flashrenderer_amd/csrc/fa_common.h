@@ -125,18 +125,15 @@ struct AttnParams {
   // per KV head (fa_prefill.hip); 0 keeps one q head per tile
   int pack_heads;
   // Append of one new token per (sequence, KV head) fused into the decode
-  // step (fa_flash_attn_paged_append_fwd). app_k / app_v [B, Hk, 1, D] go to
-  // position app_start(b) of the pages (k / v). The decode kernel takes the
-  // token's row from app_k / app_v in registers, and the combine kernel,
-  // which runs after every page read, writes it into the pages. With
-  // app_advance the position is seqlen[b] (the length before the append),
-  // the attention sees seqlen[b] + 1 keys, and the combine kernel stores
-  // seqlen[b] + 1. The kernels that take the step without the fused path
-  // (prefill path) also see seqlen[b] + 1 keys.
+  // step (fa_flash_attn_paged_append_fwd, advance mode). app_k / app_v
+  // [B, Hk, 1, D] go to position seqlen[b] of the pages (k / v), the length
+  // before the append. The decode kernel takes the token's row from app_k /
+  // app_v, and the combine kernel, which runs after every page read, writes
+  // it into the pages and stores seqlen[b] + 1. With app_advance the
+  // attention sees seqlen[b] + 1 keys, also on the kernels that take the
+  // step without the fused path (the append kernel ran first).
   const f16* app_k;              // nullptr: no fused append
   const f16* app_v;
-  const int32_t* app_positions;  // nullable [B]: start positions
-  int app_pos;                   // start position when app_positions is null
   int app_advance;               // 0 or 1
   int* ws_app;                   // [B] positions the decode kernel publishes to the combine kernel
 
@@ -154,10 +151,6 @@ struct AttnParams {
     int n = seqlen[b] + app_advance;
     n = n < 0 ? 0 : n;
     return n > N ? N : n;
-  }
-  // Position of the fused append's new token of sequence b.
-  __device__ __forceinline__ int app_start(int b) const {
-    return app_advance ? seqlen[b] : app_positions ? app_positions[b] : app_pos;
   }
   // K/V head of query head hq, or -1 if the head map points outside [0, Hk).
   __device__ __forceinline__ int kv_head(int hq) const {

@@ -209,7 +209,9 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
   for (int b = b0; b < b1; ++b) {
     const int keys = visible_keys(p, b);
     s_keys[b] = keys;
-    if (s_app != nullptr) s_app[b] = p.app_start(b);
+    // the fused kernels run in advance mode only (fa_abi.hip): the new
+    // token goes to position seqlen[b]
+    if (s_app != nullptr) s_app[b] = p.seqlen[b];
     sum += key_groups(keys) * p.Hk;
   }
   int incl = sum;  // inclusive prefix of the chunk sums within the wave
@@ -323,13 +325,13 @@ __device__ __forceinline__ SplitRange split_range(const int* units, int B, int H
 // the segment's K/V. A KV head with more than 16 * NBLK query rows (heads x
 // positions) is walked once per 16 * NBLK rows.
 //
-// APPEND (the fused append of fa_flash_attn_paged_append_fwd, without rotary
-// tables): the new token of (b, hk) at position s = app_start(b) is not read
-// from the pages, which the combine kernel writes only after this kernel. A
-// segment that holds s loads the lane's fragments of the token's K and V rows
-// before its group loop, and puts them into the group's registers in place of
-// the page row before the group is processed. Nothing here waits on the
-// append.
+// APPEND (the fused append of fa_flash_attn_paged_append_fwd in advance
+// mode, without rotary tables): the new token of (b, hk) at position
+// s = seqlen[b] is not read from the pages, which the combine kernel writes
+// only after this kernel. The wave that owns the group of s loads that group
+// and the lane's fragments of the token's K and V rows after its group loop,
+// and puts them into the group's registers in place of the page row before
+// the group is processed. Nothing here waits on the append.
 template <int D, bool ALIGNED, bool QSPLIT, int NBLK, bool APPEND>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   constexpr int KSTEPS = DecodeRegs<D>::KSTEPS;
@@ -415,18 +417,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 
     // Fused append (the step's new token at position seqlen[b], the
     // sequence's last key): its group g_app is the last group of the segment
-    // and the last of the wave that owns it. That wave loads the group into
-    // app_regs, and the token's K and V rows into app_k / app_v, at the start
-    // of the pass, and processes it after the group loop with the token's row
-    // in place of the page's. So the group loop is the plain kernel's, and
-    // the group still comes last for its wave. The token replaces the page
-    // row only where some row sees it and where the append writes it (a
+    // and the last of the wave that owns it. After the group loop that wave
+    // loads the group and the token's K and V rows, puts the token's row in
+    // place of the page's and processes the group. So the group loop is the
+    // plain kernel's, nothing of the token is held in registers across it,
+    // and the group still comes last for its wave. The token replaces the
+    // page row only where some row sees it and where the append writes it (a
     // mapped page).
     int r_app = 0;
-    u32x4 app_k[APPEND ? KSTEPS : 1];
-    uint32_t app_v[APPEND ? VW : 1];
-    constexpr int kAppRope = APPEND ? KSTEPS / 2 : 1;
-    half8 app_c[kAppRope], app_s[kAppRope];
     // With ALIGNED loads every prefetch is issued unconditionally (groups past
     // the end read as empty ranges), which keeps the number of loads in flight
     // the same on every path, so each group waits only for its own loads.
@@ -604,7 +602,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       // to its owner wave, after the loop
       int g_loop = g_end;
       bool app_owner = false;
-      DecodeRegs<D> app_regs;
       if constexpr (APPEND) {
         const int s = __builtin_amdgcn_readfirstlane(s_app[b]);
         const bool seen = s >= 0 && s < t_end && (s >> 4) >= g_begin && (s >> 4) == g_end - 1 &&
@@ -613,22 +610,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           g_loop = s >> 4;
           r_app = s & 15;
           app_owner = ((g_loop - g_begin) & (kDecodeWaves - 1)) == wave;
-        }
-        if (app_owner) {
-          load_group<D, ALIGNED>(app_regs, p, kp, vp, b, hk, g_loop << 4, t_end, n, quarter,
-                                 glane);
-          const int64_t row = ((int64_t)b * p.Hk + hk) * D;
-          // K: the lane's chunks 8*quarter + 32*kk of the row (row n of a group)
-#pragma unroll
-          for (int kk = 0; kk < KSTEPS; ++kk)
-            app_k[kk] = *reinterpret_cast<const u32x4*>(p.app_k + row + 8 * quarter + 32 * kk);
-          // V: the lane's DPL dims at DPL * n (of rows 4*quarter + i)
-          const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.app_v + row + DPL * n);
-#pragma unroll
-          for (int w2 = 0; w2 < VW; ++w2) app_v[w2] = vr[w2];
-          // chunk kk holds dims 8*quarter + 32*kk + (0..7), whose rotary
-          // partners d + D/2 are in chunk kk + KSTEPS/2 of the same lane
-          if (p.rope_cos != nullptr) rope_tables<KSTEPS, 32>(app_c, app_s, p, s, 8 * quarter);
         }
       }
       for (int g = g0; g < g_loop; g += RING * kDecodeWaves) {
@@ -645,11 +626,21 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       }
       if constexpr (APPEND) {
         if (app_owner) {
-          // K rotated at the token's position, as the append kernel rotates
-          // the row it writes; then the token's row in place of the page's
-          if (p.rope_cos != nullptr)
-            rope_rotate<KSTEPS>(reinterpret_cast<half8*>(app_k), app_c, app_s,
-                                (g_loop << 4) + r_app < p.rope_len);
+          DecodeRegs<D> app_regs;
+          load_group<D, ALIGNED>(app_regs, p, kp, vp, b, hk, g_loop << 4, t_end, n, quarter,
+                                 glane);
+          const int64_t row = ((int64_t)b * p.Hk + hk) * D;
+          // K: the lane's chunks 8*quarter + 32*kk of the row (row n of a group)
+          u32x4 app_k[KSTEPS];
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk)
+            app_k[kk] = *reinterpret_cast<const u32x4*>(p.app_k + row + 8 * quarter + 32 * kk);
+          // V: the lane's DPL dims at DPL * n (of rows 4*quarter + i)
+          uint32_t app_v[VW];
+          const uint32_t* vr = reinterpret_cast<const uint32_t*>(p.app_v + row + DPL * n);
+#pragma unroll
+          for (int w2 = 0; w2 < VW; ++w2) app_v[w2] = vr[w2];
+          // the token's row in place of the page's
           if (n == r_app) {
 #pragma unroll
             for (int kk = 0; kk < KSTEPS; ++kk) app_regs.k[kk] = app_k[kk];
@@ -772,14 +763,11 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
                                                     int64_t nthreads) {
   f16* kd = reinterpret_cast<f16*>(const_cast<void*>(p.k));
   f16* vd = reinterpret_cast<f16*>(const_cast<void*>(p.v));
-  // with rotary tables a lane moves chunk c and its rotary partner c + D/16
-  // and rotates K at its position, as paged_append_rope_kernel does
-  const bool rope = p.rope_cos != nullptr;
-  const int per_row = rope ? D / 16 : D / 8;
-  const int64_t total = (int64_t)p.B * p.Hk * per_row;
+  constexpr int kPerRow = D / 8;
+  const int64_t total = (int64_t)p.B * p.Hk * kPerRow;
   for (int64_t e = first; e < total; e += nthreads) {
-    const int64_t row = e / per_row;
-    const int c = (int)(e - row * per_row);
+    const int64_t row = e / kPerRow;
+    const int c = (int)(e - row * kPerRow);
     const int b = (int)(row / p.Hk);
     const int hk = (int)(row - (int64_t)b * p.Hk);
     const int pos = p.ws_app[b];
@@ -788,19 +776,8 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
     if (dst < 0) continue;
     const f16* ks = p.app_k + row * D;
     const f16* vs = p.app_v + row * D;
-    if (rope) {
-      half8 k2[2] = {*reinterpret_cast<const half8*>(ks + 8 * c),
-                     *reinterpret_cast<const half8*>(ks + 8 * c + D / 2)};
-      rope_fragment<2, D / 2>(k2, p, pos, 8 * c);
-      *reinterpret_cast<half8*>(kd + dst + 8 * c) = k2[0];
-      *reinterpret_cast<half8*>(kd + dst + 8 * c + D / 2) = k2[1];
-      *reinterpret_cast<u32x4*>(vd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(vs + 8 * c);
-      *reinterpret_cast<u32x4*>(vd + dst + 8 * c + D / 2) =
-          *reinterpret_cast<const u32x4*>(vs + 8 * c + D / 2);
-    } else {
-      *reinterpret_cast<u32x4*>(kd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(ks + 8 * c);
-      *reinterpret_cast<u32x4*>(vd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(vs + 8 * c);
-    }
+    *reinterpret_cast<u32x4*>(kd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(ks + 8 * c);
+    *reinterpret_cast<u32x4*>(vd + dst + 8 * c) = *reinterpret_cast<const u32x4*>(vs + 8 * c);
   }
   if (p.app_advance) {
     int32_t* sl = const_cast<int32_t*>(p.seqlen);

@@ -370,9 +370,9 @@ class PagedKVCache:
 
         The same as `append(k_new, v_new)` then `attention(q, head_map,
         causal, q_offset=lengths, rope=rope)` (the reference's decode step,
-        engine/llama_tp.py:183-200), but the lengths advance on the device and
-        the append needs no launch of its own when the attention runs on the
-        decode kernels (see flash_attn_paged_append). The query rows sit at
+        engine/llama_tp.py:183-200), but the lengths advance on the device and,
+        without rope, the append needs no launch of its own when the attention
+        runs on the decode kernels (see flash_attn_paged_append). The query rows sit at
         the new token's position (q_offset = the lengths before the step).
         """
         B, Hk, T, D = k_new.shape

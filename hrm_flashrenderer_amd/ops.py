@@ -503,13 +503,13 @@ def flash_attn_paged_append(q, k_pages, v_pages, k_new, v_new, seqlen, page_size
 
     The reference's decode step makes these two calls (cache.append,
     engine/llama_tp.py:65-78, then flash_attn_paged, :186-200). Here, with
-    start_pos=None, when the attention runs on the decode kernels with at
-    most 32 query rows per KV head (single-token decode at the benchmark
-    shapes), the append has no launch of its own. The new token is every
-    sequence's last key: the decode kernel reads it from k_new / v_new
-    (rotated there with rope), and its merge kernel writes it into the pages.
-    Other calls launch the append kernel first. Results equal the two calls'
-    in every case.
+    start_pos=None and no rope, when the attention runs on the decode kernels
+    with at most 32 query rows per KV head (single-token decode at the
+    benchmark shapes), the append has no launch of its own. The new token is
+    every sequence's last key: the decode kernel reads it from k_new / v_new,
+    and its merge kernel writes it into the pages. Other calls (rope steps
+    among them, where the separate rotary append measured faster) launch the
+    append kernel first. Results equal the two calls' in every case.
 
     k_new, v_new: fp16 [B, Hk, 1, D] (written into the pages in place).
     start_pos=None: the token of sequence b goes to position seqlen[b], the
