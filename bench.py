@@ -416,6 +416,42 @@ def bench_token_major(steps, warmup, dev, traffic, H=40, KVH=8, Dh=128, t=32767,
                          "layout": "token-major [T, KVH, Dh] fp16, fp32 q/out"}}
 
 
+def bench_contiguous_decode(steps, warmup, dev, B=8, Hq=64, Hk=8, N=16384, D=128, sets=2):
+    """flash_attn over contiguous K/V [B, Hk, N, D] with few query rows (the
+    reference serves every M with one launcher, csrc/flash_attn_sm75.cu:
+    428-467): M = 1 (non-causal) and M = 4 (causal, the last four positions)
+    at the Llama-70B head counts, on the split-K decode kernels. GB/s of the
+    K/V bytes plus q and o, rotating `sets` caches (2 x 537 MB) so that every
+    step reads HBM."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(1008)
+    caches = [(torch.randn(B, Hk, N, D, generator=g, device=dev).half(),
+               torch.randn(B, Hk, N, D, generator=g, device=dev).half()) for _ in range(sets)]
+    out = {}
+    for M, causal in ((1, False), (4, True)):
+        q = torch.randn(B, Hq, M, D, generator=g, device=dev).half()
+        qo = N - M
+        nbytes = B * Hk * N * D * 2 * 2 + 2 * B * Hq * M * D * 2
+        it = [0]
+
+        def step(ev):
+            k, v = caches[it[0] % sets]
+            it[0] += 1
+            if ev:
+                ev[0].record()
+            flash_attn(q, k, v, causal, qo, 0)
+            if ev:
+                ev[1].record()
+
+        _, mean_ms = back_to_back(step, steps, warmup)
+        out[f"M{M}"] = {"kernel_ms_back_to_back": round(mean_ms, 4), "bytes_per_step": nbytes,
+                        "roofline": roofline("hbm", nbytes, mean_ms),
+                        "causal": causal, "q_offset": qo}
+    out["workload"] = {"B": B, "Hq": Hq, "Hk": Hk, "N": N, "D": D,
+                       "path": "fa_flash_attn_fwd_ws: split-K decode kernels + combine"}
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline ---
 
 def cpu_threads():
@@ -625,6 +661,10 @@ def main():
         del w5r
     if "1" in cfgs:
         extra["cfg1_contiguous"] = bench_cfg1(K, W, dev)
+        extra["contiguous_decode"] = bench_contiguous_decode(K, W, dev)
+        log("contiguous decode: " + ", ".join(
+            f"{k} {v['roofline']['achieved']} GB/s" for k, v in extra["contiguous_decode"].items()
+            if k.startswith("M")))
     if "gemm" in cfgs:
         extra["fp16_gemm_reference"] = bench_gemm_reference(dev)
         log(f"fp16 GEMM reference: {extra['fp16_gemm_reference']['tflops']} TFLOP/s")

@@ -238,11 +238,11 @@ class PagedKVCache:
         if pos.device.type != "cpu":
             pos = pos.cpu()  # one read-back, like the reference's .item() calls
         if pos.dim() == 1:
-            if pos.numel() != T:
-                raise ValueError("positions [T] must have T entries")
+            # the reference's fast path reads positions[0] only and writes the
+            # T tokens from there (engine/llama_tp.py:67-74)
+            if T and pos.numel() == 0:
+                raise ValueError("positions [T] must hold the start position")
             start = int(pos[0]) if T else 0
-            if T and not torch.equal(pos.to(torch.int64), torch.arange(start, start + T)):
-                raise ValueError("positions [T] must be consecutive")
             return [start] * self.bsz
         if pos.dim() == 2:
             if tuple(pos.shape) != (self.bsz, T):
@@ -260,8 +260,9 @@ class PagedKVCache:
         """Write k_new / v_new `[B, Hk, T, D]` at positions start_b .. start_b+T-1.
 
         `positions`: None (append at each sequence's current length), an int
-        or a `[T]` tensor (same start for all sequences, as the reference's
-        fast path, llama_tp.py:65-78), or `[B, T]` (any positions per row,
+        or a `[T]` tensor (same start for all sequences, positions[0], as the
+        reference's fast path, llama_tp.py:65-78, which reads no other entry),
+        or `[B, T]` (any positions per row,
         the reference's general path, llama_tp.py:80-99: a row of
         consecutive positions is appended from its start, other rows are
         scattered token by token; of two tokens of one row at the same
@@ -269,6 +270,14 @@ class PagedKVCache:
         kernel launch in every case. `rope=(cos, sin)` rotates each key at
         its own position in the same launch (the reference's apply_rope on
         K, engine/llama_tp.py:183).
+
+        Lengths: each sequence's becomes max(its length, start + T). The
+        reference's fast path instead sets every sequence's length to the
+        largest end so far (cur_len, llama_tp.py:76-77). The two agree while
+        the sequences have equal lengths, which is all the reference's caller
+        produces. After ragged appends, the reference's rule would make a
+        short sequence attend slots nothing wrote; here each sequence keeps
+        its own length.
 
         `valid` (host ints, one per sequence, each <= T): only the first
         valid[b] tokens of sequence b are real (a ragged chunk padded to T);

@@ -68,9 +68,18 @@ def test_free_returns_pages_and_reset_keeps_the_pool():
     assert c.cur_len == 0
 
 
+def test_one_d_positions_use_the_first_entry():
+    """A [T] positions tensor gives every sequence the start positions[0],
+    whatever the other entries hold, as the reference's fast path reads it
+    (engine/llama_tp.py:67-69)."""
+    c = _cache()
+    assert c._starts(torch.tensor([3, 4, 6]), 3) == [3, 3, 3]
+    assert c._starts(torch.tensor([7]), 3) == [7, 7, 7]
+    assert c._starts(torch.tensor([5, 6, 7]), 3) == [5, 5, 5]
+
+
 @pytest.mark.parametrize("positions,msg", [
-    (torch.tensor([3, 4, 6]), "consecutive"),
-    (torch.tensor([1, 2]), "T entries"),
+    (torch.tensor([], dtype=torch.int64), "start position"),
     (torch.tensor([[0, 1, 2]]), "match"),
     (torch.tensor([[0, 1, 2], [5, -6, 8], [0, 1, 2]]), "non-negative"),
     (-1, "non-negative"),
