@@ -701,7 +701,10 @@ def test_full_size_prefill_cfg2_sampled_heads(gpu):
     out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True,
                            block_table=w.block_table).cpu().numpy()
     assert np.isfinite(out).all()
-    pairs = [(0, 0), (1, 17), (2, 26), (3, 39)]
+    # fp64 on the CPU: one q head of every (sequence, KV head) group, the head
+    # within the group rotating, 32 of the 160 pairs
+    group = w.Hq // w.Hk
+    pairs = [(b, hk * group + (b + hk) % group) for b in range(w.B) for hk in range(w.Hk)]
     ref = paged_reference(w.q, w.k_pool, w.v_pool, w.block_table, w.lengths, 16, w.head_map,
                           True, None, pairs=pairs)
     for (b, h), r in ref.items():
@@ -715,7 +718,11 @@ def test_full_size_chunked_prefill_cfg5_sampled_heads(gpu):
     out = flash_attn_paged(w.q, w.k_pool, w.v_pool, w.seqlen, 16, w.head_map, True,
                            w.q_offsets, block_table=w.block_table).cpu().numpy()
     assert np.isfinite(out).all()
-    pairs = [(b, (7 * b) % 64) for b in range(0, 16, 3)]
+    # fp64 on the CPU: two q heads of every sequence, on KV heads b and b + 4
+    # (mod 8) with the head within the group rotating, 32 of the 1024 pairs
+    group = w.Hq // w.Hk
+    pairs = [(b, hk * group + (3 * b + hk) % group) for b in range(w.B)
+             for hk in sorted({b % w.Hk, (b + w.Hk // 2) % w.Hk})]
     ref = paged_reference(w.q, w.k_pool, w.v_pool, w.block_table, w.lengths, 16, w.head_map,
                           True, w.q_offsets_host, pairs=pairs)
     for (b, h), r in ref.items():
