@@ -377,6 +377,50 @@ __device__ __forceinline__ float max16(const floatx16& s) {
 // the next one): a missing array reads a valid stand-in address (the first
 // word of Q) and its default replaces the value. Uniform (b, hq) give scalar
 // loads; per-lane ones give vector loads that all leave before one wait.
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by one high multiply: the
+// round-up method of Granlund and Montgomery ("Division by invariant integers
+// using multiplication", PLDI 1994). With s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1, n / d = (umulhi(n, m) + n) >> s; the sum
+// fits 32 bits because umulhi(n, m) <= n < 2^31. Built on the host, so the
+// kernel's work-item decode is a few scalar instructions instead of a
+// reciprocal and a correction sequence per division.
+struct FastDiv {
+  uint32_t m;
+  uint32_t s;
+  int d;
+};
+
+inline FastDiv make_fastdiv(int d) {
+  FastDiv f;
+  d = d < 1 ? 1 : d;  // never divided by: the entry points return before launch on empty shapes
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < (uint64_t)d) ++s;
+  f.s = s;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << s) - (uint64_t)d)) / (uint64_t)d + 1);
+  return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+  return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.s);
+}
+
+// Work list of the 128-row prefill grid, decided on the host from the shapes:
+// item = (pair, q tile, head) where a pair is one (sequence, KV-head group) of
+// `group` q heads with `ntq` q tiles each (PACKED: one (sequence, KV head) of
+// ntq packed tiles, group 1). order 0: slot L runs item
+// (L % 8) * per_xcd + L / 8 of the list ordered by (pair, q tile descending,
+// head). order 1 and 2 (the pairs divide evenly over the XCDs): XCD x owns
+// pairs x, x + 8, ..., kp of them; order 1 runs them four at a time with the
+// items interleaved, order 2 one after another with only the last tp
+// interleaved. rank: order the XCD's pairs by key count first.
+struct PrefillGrid {
+  int ntq, group, per_xcd, total;
+  int order, kp, tp, head_items, rank;
+  int per_pair, ngroups, band, gsz;
+  FastDiv d_pair, d_group, d_ngroups, d_band, d_gsz;
+};
+
 struct SeqData {
   int kv_len, hk, qo, ko, qlen;
 };
@@ -388,11 +432,13 @@ __device__ __forceinline__ int ld_or(const int32_t* ptr, int idx, int dflt, cons
   return ptr != nullptr ? v : dflt;
 }
 
-__device__ __forceinline__ SeqData seq_data(const AttnParams& p, int b, int hq) {
+// dflt_hk: q head hq's KV head when there is no head map (the contiguous
+// operator: hq / (Hq / Hk), which the caller knows from its work item).
+__device__ __forceinline__ SeqData seq_data(const AttnParams& p, int b, int hq, int dflt_hk) {
   SeqData d;
   const int n = ld_or(p.seqlen, b, p.N, p.q) + (p.seqlen != nullptr ? p.app_advance : 0);
   d.kv_len = n < 0 ? 0 : n > p.N ? p.N : n;
-  const int hk = ld_or(p.head_map, hq, p.head_mod ? hq % p.Hk : hq / p.group, p.q);
+  const int hk = ld_or(p.head_map, hq, dflt_hk, p.q);
   d.hk = (hk >= 0 && hk < p.Hk) ? hk : -1;
   d.qo = ld_or(p.q_offsets, b, p.q_offset, p.q);
   d.ko = ld_or(p.k_offsets, b, p.k_offset, p.q);
@@ -625,9 +671,7 @@ __device__ __forceinline__ void dma_slab(const QuarterSrc& q, const uint32_t* vo
 // q head). `ntq` is then the number of 128-row tiles per pair, `group` 1,
 // and slot L runs pair L / ntq (consecutive pairs go to different XCDs).
 template <int D, bool PACKED>
-__global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, int ntq,
-                                                                  int group, int per_xcd,
-                                                                  int total) {
+__global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, PrefillGrid g) {
   using C = DmaCfg<D>;
   constexpr int BN = 32;
   constexpr int NW = 4;
@@ -653,70 +697,67 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   __shared__ int s_pk_n[2];
 
   const int slot = blockIdx.x;
-  const int item = PACKED ? slot : (slot & 7) * per_xcd + (slot >> 3);
-  if (item >= total) return;
-  const int per_pair = ntq * group;
-  int pair = item / per_pair;
-  int rem = item - pair * per_pair;
-  int qt = ntq - 1 - rem / group;
-  int head = rem % group;
-  const int ngroups = PACKED ? p.Hk : p.Hq / group;
+  const int item = PACKED ? slot : (slot & 7) * g.per_xcd + (slot >> 3);
+  if (item >= g.total) return;
+  const int group = g.group;
+  const int ngroups = g.ngroups;
+  int pair, qt, head;
   // With `pre`, the sequence data of the chosen pair come from the loads that
   // ordered the pairs (kv_len_pre, hk_pre, qo_pre, ko_pre).
   bool pre = false;
   int kv_len_pre = 0, hk_pre = 0, qo_pre = 0, ko_pre = 0, qlen_pre = 0;
-  if (!PACKED && per_xcd % per_pair == 0 && total == 8 * per_xcd) {
+  if (PACKED || g.order == 0) {
+    pair = fdiv(item, g.d_pair);
+    const int rem = item - pair * g.per_pair;
+    const int r = fdiv(rem, g.d_group);
+    qt = g.ntq - 1 - r;
+    head = rem - r * group;
+  } else {
     // Each XCD owns whole (sequence, KV group) pairs: XCD x takes pairs x,
     // x + 8, x + 16, ..., so sequences of different lengths spread over all
     // XCDs.
-    const int kp = per_xcd / per_pair;
     // When the K/V of four pairs (at the per-sequence capacity) fit one XCD's
     // 4 MB L2 (cfg2: 1 MB per pair), four pairs at a time run longest q tile
-    // first across all four: the XCD's slots finish together and the four
-    // pairs share the L2 (+1.5 % on cfg2 over two at a time). Longer pairs
-    // (cfg5: up to 17 MB each) run one after another, longest q tile first
-    // within each, so a pair's items start together and stream its K/V
-    // through the L2 once; only the XCD's last two pairs interleave, to keep
-    // the tail short. On cfg5 that fetches 1.03x the algorithmic bytes
-    // against 2.0x with every two pairs interleaved, at 0.4-0.6 % of time
-    // (same-process A/B on two boxes); interleaving the last four fetched
-    // 1.22x and lost 1.6 %, and no interleave at all lost 1.0 %.
-    const bool four_fit = (int64_t)p.N * D * 2 * 2 * 4 <= ((int64_t)4 << 20);
+    // first across all four (order 1): the XCD's slots finish together and
+    // the four pairs share the L2 (+1.5 % on cfg2 over two at a time). Longer
+    // pairs (cfg5: up to 17 MB each) run one after another, longest q tile
+    // first within each (order 2), so a pair's items start together and
+    // stream its K/V through the L2 once; only the XCD's last two pairs
+    // interleave, to keep the tail short. On cfg5 that fetches 1.03x the
+    // algorithmic bytes against 2.0x with every two pairs interleaved, at
+    // 0.4-0.6 % of time (same-process A/B on two boxes); interleaving the
+    // last four fetched 1.22x and lost 1.6 %, and no interleave at all lost
+    // 1.0 %.
     const int x = slot & 7, l = slot >> 3;
     int r, w, j;
-    if (four_fit && kp % 4 == 0) {
-      const int gsz = 4 * per_pair;
-      const int gi = l / gsz, lg = l - gi * gsz;
-      const int band = 4 * group;
-      r = lg / band;
-      w = lg - r * band;
-      j = gi * 4 + w / group;
+    if (g.order == 1) {
+      const int gi = fdiv(l, g.d_gsz), lg = l - gi * g.gsz;
+      r = fdiv(lg, g.d_band);
+      w = lg - r * g.band;
+      j = gi * 4 + fdiv(w, g.d_group);
+    } else if (l < g.head_items) {
+      j = fdiv(l, g.d_pair);
+      const int lg = l - j * g.per_pair;
+      r = fdiv(lg, g.d_group);
+      w = lg - r * group;
     } else {
-      const int tp = kp >= 2 ? 2 : 1;            // pairs interleaved at the end
-      const int head_items = (kp - tp) * per_pair;
-      if (l < head_items) {
-        j = l / per_pair;
-        const int lg = l - j * per_pair;
-        r = lg / group;
-        w = lg - r * group;
-      } else {
-        const int l2 = l - head_items;
-        const int band = tp * group;
-        r = l2 / band;
-        w = l2 - r * band;
-        j = kp - tp + w / group;
-      }
+      const int l2 = l - g.head_items;
+      r = fdiv(l2, g.d_band);
+      w = l2 - r * g.band;
+      j = g.kp - g.tp + fdiv(w, g.d_group);
     }
-    if (p.seqlen != nullptr && p.q_offsets != nullptr && kp > 1 && kp <= 64) {
+    head = w - fdiv(w, g.d_group) * group;
+    if (g.rank) {
       // Chunked prefill over cached context: a pair's work grows with its
       // sequence's key count, so the XCD runs its pairs longest first. One
       // round of per-lane loads gives every candidate's key count, head map
       // entry and offsets; the chosen pair's are then read from its lane. (A
       // plain prefill batch keeps the natural order and saves this round.)
       const int lane = threadIdx.x & 63;
-      const int cpair = x + 8 * min(lane, kp - 1);
-      const SeqData c = seq_data(p, cpair / ngroups, (cpair % ngroups) * group + w % group);
-      j = pair_by_length(lane < kp ? c.kv_len : -1, kp, j);
+      const int cpair = x + 8 * min(lane, g.kp - 1);
+      const int cb = fdiv(cpair, g.d_ngroups), chk = cpair - cb * ngroups;
+      const SeqData c = seq_data(p, cb, chk * group + head, chk);
+      j = pair_by_length(lane < g.kp ? c.kv_len : -1, g.kp, j);
       kv_len_pre = __builtin_amdgcn_readlane(c.kv_len, j);
       hk_pre = __builtin_amdgcn_readlane(c.hk, j);
       qo_pre = __builtin_amdgcn_readlane(c.qo, j);
@@ -725,11 +766,10 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
       pre = true;
     }
     pair = x + 8 * j;
-    qt = ntq - 1 - r;
-    head = w % group;
+    qt = g.ntq - 1 - r;
   }
-  const int b = pair / ngroups;
-  const int hk_pair = pair % ngroups;  // PACKED: the pair's KV head
+  const int b = fdiv(pair, g.d_ngroups);
+  const int hk_pair = pair - b * ngroups;  // PACKED: the pair's KV head
   const int hq = PACKED ? 0 : hk_pair * group + head;
 
   const int tid = threadIdx.x;
@@ -774,8 +814,13 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
     pk_count = min(s_pk_n[0], p.pack_heads);
     pk_rows = pk_count * p.M;
   }
+  // The wave's block of 32 rows. Under a causal mask the block with the last
+  // rows computes up to three more tiles than the first; the per-head layout
+  // rotates the blocks over the waves from item to item so that this work
+  // does not always land on the same SIMD.
+  const int rblk = PACKED ? wave : (wave + (slot >> 3)) & (NW - 1);
   // This lane's query row: position qrow of q head hq_row.
-  const int prow = q0 + wave * 32 + col;  // PACKED: row of the pair's packed list
+  const int prow = q0 + rblk * 32 + col;  // PACKED: row of the pair's packed list
   const int pj = PACKED ? prow / p.M : 0;
   const bool row_exists = PACKED ? prow < pk_rows : true;
   const int qrow = PACKED ? prow - pj * p.M : prow;
@@ -799,7 +844,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   }
   using Table = SlabTable<D, NW, BN>;
   const typename Table::RowReq req0 = Table::row_load(p, b, lane, wave);
-  const SeqData sd = seq_data(p, b, hq);
+  const SeqData sd = seq_data(p, b, hq, hk_pair);
   const int hk = PACKED ? hk_pair : pre ? hk_pre : sd.hk;
   const int kv_len = pre ? kv_len_pre : sd.kv_len;
   const int qo = pre ? qo_pre : sd.qo;
@@ -838,7 +883,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   } else {
     const int last_row = min(q0 + kBM, qlen) - 1;
     wg_lim = head_ok && q0 < qlen ? row_key_limit(kv_len, p.causal, qo, ko, last_row) : 0;
-    const int wrow0 = q0 + wave * 32;
+    const int wrow0 = q0 + rblk * 32;
     const int wrow1 = min(wrow0 + 31, qlen - 1);
     const bool wave_rows = wrow0 < qlen;
     wave_lim_max = wave_rows ? row_key_limit(kv_len, p.causal, qo, ko, wrow1) : 0;
@@ -1017,7 +1062,7 @@ __global__ __launch_bounds__(kThreads, 3) void prefill_b32_kernel(AttnParams p, 
   const float inv = !head_ok ? __builtin_nanf("") : kv_len == 0 ? 0.f : 1.f / l_tot;
   const bool live = qrow < qlen && row_exists;  // padding rows are zeros whatever their Q held
   __syncthreads();  // every wave has finished reading the last K/V stage
-  const int lrow = wave * 32 + col;
+  const int lrow = rblk * 32 + col;
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) {
 #pragma unroll
@@ -1232,6 +1277,44 @@ static bool use_packed_rows(const AttnParams& p) {
   return p.pack_heads >= 2 && p.M < kBM && p.Hq <= kMaxPackHeads && p.Hk > 0;
 }
 
+// The work list of prefill_b32_kernel (see PrefillGrid): ntq tiles per pair,
+// `group` q heads per pair, `ngroups` pairs per sequence, `total` items.
+static PrefillGrid prefill_grid(const AttnParams& p, int D, int ntq, int group, int ngroups,
+                                int total, bool packed) {
+  PrefillGrid g{};
+  g.ntq = ntq;
+  g.group = group;
+  g.ngroups = ngroups;
+  g.total = total;
+  g.per_pair = ntq * group;
+  g.per_xcd = packed ? 0 : (total + 7) / 8;
+  g.order = 0;
+  g.tp = 1;
+  g.band = group;
+  g.gsz = g.per_pair;
+  if (!packed && g.per_xcd % g.per_pair == 0 && total == 8 * g.per_xcd) {
+    g.kp = g.per_xcd / g.per_pair;
+    const bool four_fit = (int64_t)p.N * D * 2 * 2 * 4 <= ((int64_t)4 << 20);
+    if (four_fit && g.kp % 4 == 0) {
+      g.order = 1;
+      g.gsz = 4 * g.per_pair;
+      g.band = 4 * group;
+    } else {
+      g.order = 2;
+      g.tp = g.kp >= 2 ? 2 : 1;
+      g.head_items = (g.kp - g.tp) * g.per_pair;
+      g.band = g.tp * group;
+    }
+    g.rank = p.seqlen != nullptr && p.q_offsets != nullptr && g.kp > 1 && g.kp <= 64;
+  }
+  g.d_pair = make_fastdiv(g.per_pair);
+  g.d_group = make_fastdiv(group);
+  g.d_ngroups = make_fastdiv(ngroups);
+  g.d_band = make_fastdiv(g.band);
+  g.d_gsz = make_fastdiv(g.gsz);
+  return g;
+}
+
 hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t stream) {
   if (dtype == 1) {
     const dim3 grid((unsigned)((p.M + kF32Rows - 1) / kF32Rows), (unsigned)p.Hq, (unsigned)p.B);
@@ -1254,26 +1337,21 @@ hipError_t launch_prefill(const AttnParams& p, int D, int dtype, hipStream_t str
   if (use_packed_rows(p)) {
     // (head, position) rows of each KV head packed into 128-row tiles
     const int ntp = (int)(((int64_t)p.pack_heads * p.M + kBM - 1) / kBM);
-    const int total = ntp * p.Hk * p.B;
-    const dim3 grid((unsigned)total);
+    const PrefillGrid g = prefill_grid(p, D, ntp, 1, p.Hk, ntp * p.Hk * p.B, true);
+    const dim3 grid((unsigned)g.total);
     if (D == 128)
-      hipLaunchKernelGGL((prefill_b32_kernel<128, true>), grid, dim3(kThreads), 0, stream, p, ntp, 1,
-                         0, total);
+      hipLaunchKernelGGL((prefill_b32_kernel<128, true>), grid, dim3(kThreads), 0, stream, p, g);
     else
-      hipLaunchKernelGGL((prefill_b32_kernel<64, true>), grid, dim3(kThreads), 0, stream, p, ntp, 1,
-                         0, total);
+      hipLaunchKernelGGL((prefill_b32_kernel<64, true>), grid, dim3(kThreads), 0, stream, p, g);
     return hipGetLastError();
   }
   const int group = (p.Hk > 0 && p.Hq % p.Hk == 0) ? p.Hq / p.Hk : 1;
-  const int total = ntq * p.Hq * p.B;
-  const int per_xcd = (total + 7) / 8;
-  const dim3 grid((unsigned)(8 * per_xcd));
+  const PrefillGrid g = prefill_grid(p, D, ntq, group, p.Hq / group, ntq * p.Hq * p.B, false);
+  const dim3 grid((unsigned)(8 * g.per_xcd));
   if (D == 128)
-    hipLaunchKernelGGL((prefill_b32_kernel<128, false>), grid, dim3(kThreads), 0, stream, p, ntq,
-                       group, per_xcd, total);
+    hipLaunchKernelGGL((prefill_b32_kernel<128, false>), grid, dim3(kThreads), 0, stream, p, g);
   else
-    hipLaunchKernelGGL((prefill_b32_kernel<64, false>), grid, dim3(kThreads), 0, stream, p, ntq,
-                       group, per_xcd, total);
+    hipLaunchKernelGGL((prefill_b32_kernel<64, false>), grid, dim3(kThreads), 0, stream, p, g);
   return hipGetLastError();
 }
 
