@@ -337,6 +337,7 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
     }
   }
   hipError_t e = hipSuccess;
+  bool combine_advances = false;  // the decode path's combine kernel advances the lengths
   if ((int64_t)B * Hq * M == 0) {
     // nothing to attend: the append alone
     if (p.app_k != nullptr) {
@@ -393,13 +394,16 @@ static int paged_fwd(const void* q, const void* k_pages, const void* v_pages,
       pc.dec_wgs = fa::decode_launch_wgs(cplan, pc, D);
       e = fa::launch_decode(pc, D, (hipStream_t)stream);
     }
+    combine_advances = true;
   } else {
     // the prefill kernel packs the rows of a KV head's q heads (at most
     // heads_per_kv of them) into shared 128-row tiles when M < 128
     p.pack_heads = heads_per_kv > 0 ? std::min(heads_per_kv, Hq) : 0;
     e = fa::launch_prefill(p, D, FA_DTYPE_F16, (hipStream_t)stream);
   }
-  if (e == hipSuccess && app != nullptr && app->advance && p.app_k == nullptr)
+  // the decode path's combine kernel advances the lengths itself (from the
+  // copy the decode kernel published); the other paths need a launch
+  if (e == hipSuccess && app != nullptr && app->advance && !combine_advances)
     e = fa::launch_advance_lengths(const_cast<int32_t*>(seqlen), B, (hipStream_t)stream);
   return launch_status(e);
 }

@@ -373,6 +373,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     for (int b = tid; b <= p.B; b += kDecodeThreads) {
       p.ws_units[b] = s_units[b];
       if (APPEND && b < p.B) p.ws_app[b] = s_app[b];
+      // an advance step whose token the append kernel wrote first: the
+      // combine kernel bumps the lengths from this copy
+      if (!APPEND && p.app_advance && b < p.B) p.ws_app[b] = p.seqlen[b];
     }
   }
   const int P = split_cost_p(p, U, W);
@@ -755,16 +758,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
 // kernel runs after every read of the pages. Row (b, hk) of app_k / app_v
 // goes to position ws_app[b] of the pages, one 16-byte chunk per lane,
 // skipped where the page is not mapped or beyond the capacity, as
-// paged_append_kernel skips it. With app_advance, seqlen[b] becomes
-// ws_app[b] + 1. `first` and `nthreads` give this thread's lanes of the
-// grid-stride loop.
+// paged_append_kernel skips it (no rows when app_k is null: the append
+// kernel wrote them before the decode kernel). With app_advance, seqlen[b]
+// becomes ws_app[b] + 1, the length the decode kernel read plus the token.
+// `first` and `nthreads` give this thread's lanes of the grid-stride loop.
 template <int D>
 __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t first,
                                                     int64_t nthreads) {
   f16* kd = reinterpret_cast<f16*>(const_cast<void*>(p.k));
   f16* vd = reinterpret_cast<f16*>(const_cast<void*>(p.v));
   constexpr int kPerRow = D / 8;
-  const int64_t total = (int64_t)p.B * p.Hk * kPerRow;
+  const int64_t total = p.app_k != nullptr ? (int64_t)p.B * p.Hk * kPerRow : 0;
   for (int64_t e = first; e < total; e += nthreads) {
     const int64_t row = e / kPerRow;
     const int c = (int)(e - row * kPerRow);
@@ -826,10 +830,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
   }
   const int ri = rank * p.M + qi;
   float result[DPW];
-  // With the fused append's advance, this kernel advances seqlen: the key
-  // count comes from the position the decode kernel published.
-  const int kv_len = p.app_k != nullptr && p.app_advance ? min(max(p.ws_app[b] + 1, 0), p.N)
-                                                        : p.kv_len(b);
+  // With an advance step, this kernel advances seqlen: the key count comes
+  // from the length the decode kernel published.
+  const int kv_len = p.app_advance ? min(max(p.ws_app[b] + 1, 0), p.N) : p.kv_len(b);
   if (qi >= p.q_len(b)) {
     // padding row (q_lens): zeros
 #pragma unroll
@@ -1088,8 +1091,9 @@ DecodePlan plan_decode(int B, int Hq, int M, int D, int Hk, int capacity_tokens,
 template <int D>
 void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
   int64_t app_wgs = 0;
-  if (p.app_k != nullptr) {
-    const int64_t lanes = (int64_t)p.B * p.Hk * (D / 8);
+  if (p.app_k != nullptr || p.app_advance) {
+    // page rows (fused append) or only the lengths (advance after the append kernel)
+    const int64_t lanes = p.app_k != nullptr ? (int64_t)p.B * p.Hk * (D / 8) : (int64_t)p.B;
     app_wgs = std::min<int64_t>(1024, std::max<int64_t>(1, (lanes + 255) / 256));
   }
   if (rows <= 512)
