@@ -353,7 +353,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   __shared__ float s_l[2][kRows];
   __shared__ float s_o[2][kRows][OPAD];
 
-  const int w = blockIdx.x;
+  // The piece of the split this workgroup takes. Dispatch places workgroup
+  // blockIdx on XCD blockIdx % 8, so XCD x takes pieces [x * W/8, (x+1) * W/8):
+  // neighbouring pieces (the same KV heads and sequences) share an XCD
+  // (token-major step +1.0 %, cfg4 +0.3 %, cfg3 +-0, same process). The
+  // mapping is a bijection when 8 divides W, else the identity; the combine
+  // kernel needs only the piece index.
+  const int w = (gridDim.x & 7) == 0
+                    ? (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3))
+                    : (int)blockIdx.x;
   const int W = gridDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
