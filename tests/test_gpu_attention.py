@@ -209,11 +209,16 @@ def test_decode_batch_beyond_2048_sequences(gpu, per_sequence):
     assert_close(out.cpu().numpy(), ref, f"B={B} per_sequence={per_sequence}")
 
 
-def test_fused_decode_step_beyond_2048_sequences(gpu):
+@pytest.mark.parametrize("rope", [False, True])
+def test_fused_decode_step_beyond_2048_sequences(gpu, rope):
     """The fused decode step (advance mode) over 2100 sequences: output, pages
-    and lengths bit for bit those of append + attention."""
+    and lengths bit for bit those of append + attention. Without rotary tables
+    the decode kernels take the token; with them the rotary append runs first
+    and each launch's combine kernel advances its slice of the lengths."""
     from hrm_flashrenderer_amd import flash_attn_paged_append
+    from hrm_flashrenderer_amd.rope import build_rope_cache
     B, Hq, Hk, D = 2100, 8, 2, 64
+    ropet = build_rope_cache(128, D, device=gpu) if rope else None
     g = torch.Generator().manual_seed(78)
     old = torch.randint(0, 64, (B,), generator=g).tolist()
     kp, vp, bt = _many_sequences(B, Hq, Hk, D, [n + 1 for n in old], 7800)
@@ -224,10 +229,12 @@ def test_fused_decode_step_beyond_2048_sequences(gpu):
     hm = (torch.arange(Hq) // (Hq // Hk)).to(torch.int32).to(gpu)
     old_t = torch.tensor(old, dtype=torch.int32, device=gpu)
     kr, vr = kp.clone(), vp.clone()
-    paged_kv_append(kr, vr, k_new, v_new, old_t, 16, block_table=bt)
-    o_ref = flash_attn_paged(q, kr, vr, old_t + 1, 16, hm, False, block_table=bt)
+    paged_kv_append(kr, vr, k_new, v_new, old_t, 16, block_table=bt, rope=ropet)
+    o_ref = flash_attn_paged(q, kr, vr, old_t + 1, 16, hm, False, old_t, block_table=bt,
+                             rope=ropet)
     sl = old_t.clone()
-    o = flash_attn_paged_append(q, kp, vp, k_new, v_new, sl, 16, hm, block_table=bt)
+    o = flash_attn_paged_append(q, kp, vp, k_new, v_new, sl, 16, hm, False, old_t,
+                                block_table=bt, rope=ropet)
     torch.cuda.synchronize()
     assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
     assert torch.equal(kp.view(torch.int16), kr.view(torch.int16))
