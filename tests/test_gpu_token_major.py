@@ -24,7 +24,10 @@ def _case(T, KVH, Dh, H, seed, gpu):
     return q, k, v
 
 
-@pytest.mark.parametrize("H,KVH,Dh", [(40, 8, 128), (64, 8, 128), (32, 32, 64), (14, 2, 64)])
+# (12, 3): a KV-head count that does not divide the workgroup count evenly;
+# (72, 8): 9 query heads per KV head.
+@pytest.mark.parametrize("H,KVH,Dh", [(40, 8, 128), (64, 8, 128), (32, 32, 64), (14, 2, 64),
+                                      (12, 3, 64), (72, 8, 128)])
 @pytest.mark.parametrize("t", [0, 1, 15, 16, 17, 255, 1000, 4095])
 def test_token_major_decode_matches_oracle(gpu, H, KVH, Dh, t):
     T = t + 9
