@@ -256,6 +256,12 @@ __device__ __forceinline__ int64_t mul_div_floor(int64_t x, int64_t y, int64_t z
   return (int64_t)(n / (uint64_t)z);
 }
 
+// floor(n / d) for 0 <= n < 2^63, d > 0: a 32-bit division when both fit.
+__device__ __forceinline__ int64_t div_floor(int64_t n, int64_t d) {
+  if (((uint64_t)n >> 32) == 0 && ((uint64_t)d >> 32) == 0) return (int64_t)((uint32_t)n / (uint32_t)d);
+  return n / d;
+}
+
 // Units [u0, u1) of workgroup w under the cost split: u0 is the smallest unit
 // whose cost is at least floor(w * C / W) (U for w == W), and units[b0] <= u0.
 // Segment j = b * Hk + hk starts at cost units[b] + hk * G_b + P * j (G_b
@@ -780,7 +786,7 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
   for (int64_t e = first; e < total; e += nthreads) {
     const int64_t row = e / kPerRow;
     const int c = (int)(e - row * kPerRow);
-    const int b = (int)(row / p.Hk);
+    const int b = (int)((uint32_t)row / (uint32_t)p.Hk);  // row < B * Hk < 2^31
     const int hk = (int)(row - (int64_t)b * p.Hk);
     const int pos = p.ws_app[b];
     if (pos < 0) continue;
@@ -869,8 +875,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
     const int64_t C = (int64_t)U + (int64_t)P * p.B * p.Hk;
     const int64_t seg_cost = (int64_t)P * (b * p.Hk + hk);
     if (G > 0) {
-      const int wa = (int)min((int64_t)W - 1, ((US + seg_cost + 1) * W - 1) / C);
-      const int wb = (int)min((int64_t)W - 1, ((UE + seg_cost) * W - 1) / C);
+      const int wa = (int)min((int64_t)W - 1, div_floor((US + seg_cost + 1) * W - 1, C));
+      const int wb = (int)min((int64_t)W - 1, div_floor((UE + seg_cost) * W - 1, C));
       const int first = WIDE ? wa + wave : wa;
       constexpr int STEP = WIDE ? 4 : 1;
       // Slots in batches with every load issued before the merge (8 per wave
@@ -883,7 +889,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
           const int w = w0 + i * STEP;
-          const bool live = w <= wb && (int64_t)w * C / W != (int64_t)(w + 1) * C / W;
+          // a piece's cost range is empty only when the cost is below the
+          // piece count (C < W): the divisions are skipped otherwise
+          const bool live =
+              w <= wb && (C >= W || mul_div_floor(w, C, W) != mul_div_floor(w + 1, C, W));
           const int64_t srow = rbase + (int64_t)w * p.dec_rows;
           pm[i] = live ? p.ws_ml[srow * 2] : -INFINITY;
           pl[i] = live ? p.ws_ml[srow * 2 + 1] : 0.f;
