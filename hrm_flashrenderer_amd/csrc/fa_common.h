@@ -82,6 +82,34 @@ struct KVMap {
   }
 };
 
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by one high multiply: the
+// round-up method of Granlund and Montgomery ("Division by invariant integers
+// using multiplication", PLDI 1994). With s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1, n / d = (umulhi(n, m) + n) >> s; the sum
+// fits 32 bits because umulhi(n, m) <= n < 2^31. Built on the host, so the
+// kernels' index arithmetic is a few instructions instead of a reciprocal
+// and a correction sequence per division.
+struct FastDiv {
+  uint32_t m;
+  uint32_t s;
+  int d;
+};
+
+inline FastDiv make_fastdiv(int d) {
+  FastDiv f;
+  d = d < 1 ? 1 : d;  // never divided by: the entry points return before launch on empty shapes
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < (uint64_t)d) ++s;
+  f.s = s;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << s) - (uint64_t)d)) / (uint64_t)d + 1);
+  return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+  return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.s);
+}
+
 // Per-call arguments of the attention kernels (both contiguous and paged).
 struct AttnParams {
   const void* q;      // [B, Hq, M, D]
@@ -110,6 +138,8 @@ struct AttnParams {
   int dec_wgs;          // workgroups of the decode kernel
   int dec_seg_cost;     // units charged per segment start in the decode split (fa_decode.hip)
   int dec_rows;         // row capacity of a slot: heads_per_kv * M
+  FastDiv dec_wdiv;     // dec_wgs and Hk as divisors (set by launch_decode)
+  FastDiv hk_div;
   // optional rotary embedding of Q at load time (nullptr: none): fp16 tables
   // [rope_len, D/2]; query row i of sequence b sits at position q_off(b) + i
   const f16* rope_cos;

@@ -203,6 +203,18 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
                                             int* s_keys, int* s_app) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  if (p.B == 1) {
+    // one sequence (the token-major step): no scan
+    if (tid == 0) {
+      const int keys = visible_keys(p, 0);
+      s_keys[0] = keys;
+      if (s_app != nullptr) s_app[0] = p.seqlen[0];
+      s_units[0] = 0;
+      s_units[1] = key_groups(keys) * p.Hk;
+    }
+    __syncthreads();
+    return;
+  }
   const int chunk = (p.B + kDecodeThreads - 1) / kDecodeThreads;
   const int b0 = tid * chunk, b1 = min(p.B, b0 + chunk);
   int sum = 0;
@@ -277,10 +289,13 @@ struct SplitRange {
   int u0, u1, b0;
 };
 __device__ __forceinline__ SplitRange split_range(const int* units, int B, int Hk, int U, int W,
-                                                  int P, int w) {
+                                                  int P, int w, const FastDiv& wdiv) {
   const int64_t C = (int64_t)U + (int64_t)P * B * Hk;
-  const int64_t T0 = mul_div_floor(w, C, W);
-  const int64_t T1 = mul_div_floor(w + 1, C, W);
+  // floor(w * C / W) by the multiplicative inverse of W while (w + 1) * C
+  // stays below 2^31, else by a division
+  const bool small = C * W < ((int64_t)1 << 31);
+  const int64_t T0 = small ? fdiv((int)(w * C), wdiv) : mul_div_floor(w, C, W);
+  const int64_t T1 = small ? fdiv((int)((w + 1) * C), wdiv) : mul_div_floor(w + 1, C, W);
   const int lane = threadIdx.x & 63;
   int n0 = 0, n1 = 0;  // sequences b >= 1 with cs(b) <= T0, T1
   for (int base = 1; base < B; base += 64) {
@@ -393,7 +408,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     }
   }
   const int P = split_cost_p(p, U, W);
-  const SplitRange range = split_range(s_units, p.B, p.Hk, U, W, P, w);
+  const SplitRange range = split_range(s_units, p.B, p.Hk, U, W, P, w, p.dec_wdiv);
   // The range is wave-uniform; the LDS reads it comes from leave it in VGPRs,
   // and the buffer resources built from it would then be rebuilt per lane
   // (a readfirstlane loop around every K/V load).
@@ -755,7 +770,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   int b = __builtin_amdgcn_readfirstlane(range.b0);
   for (int u = u0; u < u1;) {
     while (s_units[b + 1] <= u) ++b;
-    const int G = (s_units[b + 1] - s_units[b]) / p.Hk;
+    const int G = fdiv(s_units[b + 1] - s_units[b], p.hk_div);
     const int rel = u - s_units[b];
     const int hk = rel / G;
     const int g_lo = rel - hk * G;
@@ -1121,7 +1136,10 @@ void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
                        dim3((unsigned)((rows + 3) / 4 + app_wgs)), dim3(256), 0, stream, p);
 }
 
-hipError_t launch_decode(const AttnParams& p, int D, hipStream_t stream) {
+hipError_t launch_decode(const AttnParams& p_in, int D, hipStream_t stream) {
+  AttnParams p = p_in;
+  p.dec_wdiv = make_fastdiv(p.dec_wgs);
+  p.hk_div = make_fastdiv(p.Hk);
   const dim3 grid((unsigned)p.dec_wgs);
   const int rows = p.B * p.Hq * p.M;
   const DecodeVariant var = decode_variant(p);

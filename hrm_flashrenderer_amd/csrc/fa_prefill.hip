@@ -377,33 +377,6 @@ __device__ __forceinline__ float max16(const floatx16& s) {
 // the next one): a missing array reads a valid stand-in address (the first
 // word of Q) and its default replaces the value. Uniform (b, hq) give scalar
 // loads; per-lane ones give vector loads that all leave before one wait.
-// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by one high multiply: the
-// round-up method of Granlund and Montgomery ("Division by invariant integers
-// using multiplication", PLDI 1994). With s = ceil(log2 d) and
-// m = floor(2^32 (2^s - d) / d) + 1, n / d = (umulhi(n, m) + n) >> s; the sum
-// fits 32 bits because umulhi(n, m) <= n < 2^31. Built on the host, so the
-// kernel's work-item decode is a few scalar instructions instead of a
-// reciprocal and a correction sequence per division.
-struct FastDiv {
-  uint32_t m;
-  uint32_t s;
-  int d;
-};
-
-inline FastDiv make_fastdiv(int d) {
-  FastDiv f;
-  d = d < 1 ? 1 : d;  // never divided by: the entry points return before launch on empty shapes
-  f.d = d;
-  uint32_t s = 0;
-  while ((1ull << s) < (uint64_t)d) ++s;
-  f.s = s;
-  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << s) - (uint64_t)d)) / (uint64_t)d + 1);
-  return f;
-}
-
-__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
-  return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.s);
-}
 
 // Work list of the 128-row prefill grid, decided on the host from the shapes:
 // item = (pair, q tile, head) where a pair is one (sequence, KV-head group) of
