@@ -13,7 +13,9 @@ configuration 4 (Llama-70B shape, B=64, context U[1024,16384], 64/8 heads):
 a step appends one token per sequence and then runs decode attention over the
 full context; decode GB/s counts live K/V + q/o + block-table bytes.
 Configurations 3, 5 and 1 are reported under "extra", with "5r" (cfg5 with
-ragged chunks, timed with and without q_lens).
+ragged chunks, timed with and without q_lens). "gemm" adds two vendor
+references on the same GPU: an fp16 GEMM (hipBLASLt) and PyTorch's own flash
+attention (SDPA, flash backend) on cfg2's shape.
 
 Per-kernel durations come from HIP events recorded on the stream the kernels
 run on (torch's current stream). `roofline.achieved` is algorithmic work per
@@ -360,6 +362,55 @@ def bench_gemm_reference(dev, n=8192, iters=20):
             "shape": f"{n}x{n}x{n} fp16, fp32 accumulate", "library": "torch.matmul (hipBLASLt)"}
 
 
+def bench_vendor_attention_reference(dev, iters=30):
+    """PyTorch's own flash attention (scaled_dot_product_attention restricted
+    to its flash backend, AOTriton on ROCm) on cfg2's shape as contiguous
+    fp16 tensors (B=4, 40/8 heads, S=2048, D=128, causal, GQA), beside this
+    library's contiguous entry on the same tensors. Flops counted as for
+    cfg2 (4*D per visible pair). Reported only; not part of the attention
+    path. The math backend is never allowed: the call raises instead."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import torch.nn.functional as F
+    B, Hq, Hk, S, D = 4, 40, 8, 2048, 128
+    flops = workloads.causal_flops_contiguous(B, Hq, S, S, D)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    q = torch.randn(B, Hq, S, D, generator=g, device=dev).half()
+    k = torch.randn(B, Hk, S, D, generator=g, device=dev).half()
+    v = torch.randn(B, Hk, S, D, generator=g, device=dev).half()
+
+    def mean_ms(fn):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.1:
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    ours_ms = mean_ms(lambda: flash_attn(q, k, v, True))
+    res = {"shape": f"q [{B},{Hq},{S},{D}], k/v [{B},{Hk},{S},{D}] fp16, causal",
+           "this_library_contiguous": {"ms": round(ours_ms, 4),
+                                       "tflops": round(flops / ours_ms / 1e9, 1)}}
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            fn = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True,  # noqa: E731
+                                                        enable_gqa=True)
+            diff = (fn().float() - flash_attn(q, k, v, True).float()).abs().max().item()
+            ms = mean_ms(fn)
+        res["torch_sdpa_flash"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
+                                   "max_abs_diff_vs_this_library": diff,
+                                   "library": f"torch {torch.__version__} SDPA flash backend"}
+        res["speedup_over_torch_sdpa_flash"] = round(ms / ours_ms, 2)
+    except RuntimeError as e:
+        res["torch_sdpa_flash"] = {"unavailable": str(e)[:200]}
+    return res
+
+
 def bench_cfg1(steps, warmup, dev):
     res = {}
     for dt in (torch.float16, torch.float32):
@@ -668,6 +719,8 @@ def main():
     if "gemm" in cfgs:
         extra["fp16_gemm_reference"] = bench_gemm_reference(dev)
         log(f"fp16 GEMM reference: {extra['fp16_gemm_reference']['tflops']} TFLOP/s")
+        extra["vendor_flash_attention_reference"] = bench_vendor_attention_reference(dev)
+        log(f"vendor flash attention reference: {extra['vendor_flash_attention_reference']}")
     if "tm" in cfgs:
         extra["int8_engine_decode_token_major"] = bench_token_major(K, W, dev, traffic)
         log(f"token-major decode: "
