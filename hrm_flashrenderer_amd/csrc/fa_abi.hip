@@ -554,12 +554,40 @@ static int token_major_hpk(int H, int KVH, int heads_per_kv, bool engine_map) {
   return heads_per_kv <= 0 || heads_per_kv > H ? H : heads_per_kv;
 }
 
+// The token-major step's decode plan. Its segments serve KV heads in pairs
+// (AttnParams::kv_pair) when the head count is even and a pair's query rows
+// fit one 16-row block (two heads of at most 8 query heads each): then Hk
+// counts the pairs, a slot holds both heads' rows, and a segment has twice
+// the 16-key groups (capacity passed as 32 keys per group of the sequence).
+struct TokenMajorPlan {
+  fa::DecodePlan plan;
+  int pair;
+};
+static TokenMajorPlan token_major_plan(int H, int KVH, int Dh, int n_keys, int hpk) {
+  TokenMajorPlan t;
+  t.pair = KVH % 2 == 0 && 2 * hpk <= 16 ? 1 : 0;
+  if (t.pair) {
+    const int64_t cap = (int64_t)32 * ((n_keys + 15) / 16);
+    t.plan = fa::plan_decode(1, H, 1, Dh, KVH / 2, cap > INT_MAX ? INT_MAX : (int)cap, 2 * hpk);
+  } else {
+    t.plan = fa::plan_decode(1, H, 1, Dh, KVH, n_keys, hpk);
+  }
+  return t;
+}
+
 size_t fa_decode_token_major_workspace_bytes(int H, int KVH, int Dh, int t_max,
                                              int heads_per_kv) {
   if (H <= 0 || KVH <= 0 || !head_dim_ok(Dh) || t_max < 0 || t_max >= INT_MAX) return 0;
   if (!fa::use_decode_path(1, 1, H, KVH, 0)) return 0;
+  // the larger of the plans a launch may take (without a head map the bound
+  // is ceil(H / KVH), which is at most the one assumed here)
   const int hpk = token_major_hpk(H, KVH, heads_per_kv, false);
-  return fa::plan_decode(1, H, 1, Dh, KVH, t_max + 1, hpk).ws_bytes;
+  size_t need = token_major_plan(H, KVH, Dh, t_max + 1, hpk).plan.ws_bytes;
+  if (heads_per_kv <= 0) {
+    const int hpk_engine = token_major_hpk(H, KVH, 0, true);
+    need = std::max(need, token_major_plan(H, KVH, Dh, t_max + 1, hpk_engine).plan.ws_bytes);
+  }
+  return need;
 }
 
 int fa_decode_token_major(float* out, const float* q, const void* k_cache, const void* v_cache,
@@ -607,9 +635,11 @@ int fa_decode_token_major(float* out, const float* q, const void* k_cache, const
   p.scale_log2 = scale * fa::kLog2e;
 
   (void)hipGetLastError();
-  const fa::DecodePlan plan =
-      fa::plan_decode(1, H, 1, Dh, KVH, p.N,
-                      token_major_hpk(H, KVH, heads_per_kv, head_map == nullptr));
+  const TokenMajorPlan tp = token_major_plan(
+      H, KVH, Dh, p.N, token_major_hpk(H, KVH, heads_per_kv, head_map == nullptr));
+  const fa::DecodePlan& plan = tp.plan;
+  p.kv_pair = tp.pair;
+  p.Hk = KVH >> tp.pair;
   if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
     return fail(FA_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu", plan.ws_bytes,
                 workspace == nullptr ? (size_t)0 : workspace_bytes);

@@ -150,6 +150,10 @@ struct AttnParams {
   int q_f32;
   int o_f32;
   int head_mod;
+  // decode with the fp32-query split only: 1 when each segment serves a pair
+  // of KV heads (2j, 2j + 1), alternating their 16-key groups; Hk then counts
+  // the pairs, and kv_head() gives a q head's pair (kv_head_real() its head)
+  int kv_pair;
   // prefill with M < 128 rows per q head: > 0 packs the (head, position) rows
   // of each KV head's q heads into 128-row tiles, at most pack_heads heads
   // per KV head (fa_prefill.hip); 0 keeps one q head per tile
@@ -182,11 +186,23 @@ struct AttnParams {
     n = n < 0 ? 0 : n;
     return n > N ? N : n;
   }
-  // K/V head of query head hq, or -1 if the head map points outside [0, Hk).
+  // K/V head of query head hq, or -1 if the head map points outside the
+  // heads; with kv_pair, the head's pair.
   __device__ __forceinline__ int kv_head(int hq) const {
-    if (head_map == nullptr) return head_mod ? hq % Hk : hq / group;
+    if (kv_pair == 0) {
+      if (head_map == nullptr) return head_mod ? hq % Hk : hq / group;
+      int hk = head_map[hq];
+      return (hk >= 0 && hk < Hk) ? hk : -1;
+    }
+    const int r = kv_head_real(hq);
+    return r < 0 ? -1 : r >> 1;
+  }
+  // The K/V head itself (the same as kv_head without kv_pair).
+  __device__ __forceinline__ int kv_head_real(int hq) const {
+    const int nh = Hk << kv_pair;
+    if (head_map == nullptr) return head_mod ? hq % nh : hq / group;
     int hk = head_map[hq];
-    return (hk >= 0 && hk < Hk) ? hk : -1;
+    return (hk >= 0 && hk < nh) ? hk : -1;
   }
 };
 

@@ -210,7 +210,7 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
       s_keys[0] = keys;
       if (s_app != nullptr) s_app[0] = p.seqlen[0];
       s_units[0] = 0;
-      s_units[1] = key_groups(keys) * p.Hk;
+      s_units[1] = (key_groups(keys) << p.kv_pair) * p.Hk;
     }
     __syncthreads();
     return;
@@ -224,7 +224,7 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
     // the fused kernels run in advance mode only (fa_abi.hip): the new
     // token goes to position seqlen[b]
     if (s_app != nullptr) s_app[b] = p.seqlen[b];
-    sum += key_groups(keys) * p.Hk;
+    sum += (key_groups(keys) << p.kv_pair) * p.Hk;  // a pair's segment holds both heads' groups
   }
   int incl = sum;  // inclusive prefix of the chunk sums within the wave
 #pragma unroll
@@ -239,7 +239,7 @@ __device__ __forceinline__ void unit_prefix(const AttnParams& p, int* s_units, i
   int run = base + incl - sum;
   for (int b = b0; b < b1; ++b) {
     s_units[b] = run;
-    run += key_groups(s_keys[b]) * p.Hk;
+    run += (key_groups(s_keys[b]) << p.kv_pair) * p.Hk;
   }
   if (tid == kDecodeThreads - 1) s_units[p.B] = base + incl;
   __syncthreads();
@@ -393,7 +393,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
   // The head map is read once, in the same round trip as the key counts of
   // the unit prefix (Hq <= kMaxHeads = one head per thread), so a segment's
   // head scan below reads LDS instead of waiting on memory.
-  const int my_hk = tid < p.Hq ? p.kv_head(tid) : -1;
+  // (the KV head itself: with kv_pair, a segment's rows are its pair's heads)
+  const int my_hk = tid < p.Hq ? p.kv_head_real(tid) : -1;
   unit_prefix(p, s_units, s_part, s_keys, APPEND ? s_app : nullptr);
   s_hmap[tid] = my_hk;
   __syncthreads();
@@ -427,8 +428,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     // needs them (causal limits, rotary positions).
     const int qo = p.causal || p.rope_cos != nullptr ? p.q_off(b) : 0;
     const int ko = p.causal ? p.k_off(b) : 0;
-    const int t_end = min(s_keys[b], g_stop << 4);
     const int g_end = g_stop;
+    // KV-head pairs (fp32-query split only): group g of the segment holds
+    // keys 16 (g >> 1) .. of KV head 2 hk + (g & 1). One KV head's keys of the
+    // token-major cache fall on a subset of the memory channels, and some
+    // subsets serve more slowly (at the INT8 engine's shape two heads of
+    // eight ended 5 us after the others); two heads per segment even out
+    // the rates.
+    const bool pair = QSPLIT && p.kv_pair != 0;
+    const int t_end = pair ? s_keys[b] : min(s_keys[b], g_stop << 4);
+    auto g_head = [&](int g) { return pair ? 2 * hk + (g & 1) : hk; };
+    auto g_key0 = [&](int g) { return pair ? (g >> 1) << 4 : g << 4; };
+    // key limit of group g's loads: past the segment nothing is read
+    auto g_lim = [&](int g) { return pair && g >= g_end ? 0 : t_end; };
 
     // Groups g_begin + wave + 4k of the segment go through a ring of RING
     // register sets: RING - 1 groups are in flight while one is processed.
@@ -465,7 +477,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       for (int i = 0; i < RING - 1; ++i) {
         const int gi = g0 + i * kDecodeWaves;
         if (ALIGNED || gi < g_end)
-          load_group<D, ALIGNED>(ring[i], p, kp, vp, b, hk, gi << 4, t_end, n, quarter, glane);
+          load_group<D, ALIGNED>(ring[i], p, kp, vp, b, g_head(gi), g_key0(gi), g_lim(gi), n,
+                                 quarter, glane);
       }
     };
     prefetch();
@@ -475,7 +488,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       int count = 0;
       for (int base = 0; base < p.Hq; base += 64) {
         const int hq = base + lane;
-        const bool match = hq < p.Hq && s_hmap[hq] == hk;
+        const bool match = hq < p.Hq && (s_hmap[hq] >> (pair ? 1 : 0)) == hk;
         const uint64_t mask = __ballot(match);
         if (match) {
           const int pos = count + __popcll(mask & ((1ull << lane) - 1ull));
@@ -498,6 +511,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       half8 qreg[NBLK][KSTEPS];
       half8 qlo[NBLK][QSPLIT ? KSTEPS : 1];
       float crow[NBLK];             // score scale of this lane's row (log2 units)
+      int row_par[NBLK];            // with KV-head pairs: which head of the pair the row reads
       float m_ref[NBLK];            // scaled (log2) reference max of the row
       float l_run[NBLK];
       floatx4 acc_o[NBLK][DPL];
@@ -511,6 +525,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
         const int hq = row_ok ? s_heads[ridx / p.M] : 0;
         const int qi = row_ok ? ridx % p.M : 0;
         row_lim[bk] = t_end;
+        row_par[bk] = pair ? (s_hmap[hq] & 1) : 0;
         if (p.causal) {
           int64_t lim = (int64_t)qo + qi - ko + 1;
           if (lim < row_lim[bk]) row_lim[bk] = lim < 0 ? 0 : (int)lim;
@@ -570,7 +585,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
       // One 16-token group: S^T on the matrix cores, online softmax with a lazy
       // reference max (O is rescaled only when the max grows by more than 2^8),
       // then O^T += V^T P^T with the in-lane V transpose.
-      auto process = [&](const DecodeRegs<D>& r, int t0) {
+      auto process = [&](const DecodeRegs<D>& r, int t0, int gpar) {
         half4 pb[NBLK];
 #pragma unroll
         for (int bk = 0; bk < NBLK; ++bk) {
@@ -588,10 +603,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
                                                          qlo[bk][kk], s, 0, 0, 0);
             }
           }
-          // lane holds tokens t0 + 4*quarter + i of row n
+          // lane holds tokens t0 + 4*quarter + i of row n; with KV-head pairs
+          // a group of the pair's other head is invisible to the row
+          const int lim = !pair || gpar == row_par[bk] ? row_lim[bk] : 0;
           float sv[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < row_lim[bk] ? s[i] : -INFINITY;
+          for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * quarter + i < lim ? s[i] : -INFINITY;
           const float gmax =
               wave_max16x(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * crow[bk];
           if (__builtin_amdgcn_ballot_w64(gmax > m_ref[bk] + 8.f) != 0) {
@@ -651,9 +668,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
           if (gi >= g_loop) break;
           const int gl = gi + (RING - 1) * kDecodeWaves;
           if (ALIGNED || gl < g_loop)
-            load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, hk, gl << 4, t_end, n,
-                                   quarter, glane);
-          process(ring[i], gi << 4);
+            load_group<D, ALIGNED>(ring[(i + RING - 1) % RING], p, kp, vp, b, g_head(gl),
+                                   g_key0(gl), g_lim(gl), n, quarter, glane);
+          process(ring[i], g_key0(gi), gi & 1);
         }
       }
       if constexpr (APPEND) {
@@ -686,7 +703,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
               }
             }
           }
-          process(app_regs, g_loop << 4);
+          process(app_regs, g_loop << 4, 0);
         }
       }
       (void)VW;
@@ -822,11 +839,12 @@ __device__ __forceinline__ void fused_append_writes(const AttnParams& p, int64_t
 // workgroups whose unit range meets the row's segment are recomputed from the
 // unit prefix the decode kernel stored.
 // WIDE = false: one wave per row, four rows per workgroup. WIDE = true (few
-// rows, each with many slots, as with one long sequence): one workgroup per
-// row, wave w merges slots wa + w, wa + w + 4, ..., and wave 0 merges the four
-// states.
+// rows, each with many slots, as with one long sequence): one workgroup of
+// kWideWaves waves per row, wave w merges slots wa + w, wa + w + kWideWaves,
+// ..., and wave 0 merges the waves' states.
+constexpr int kWideWaves = 8;
 template <int D, bool WIDE>
-__global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
+__global__ __launch_bounds__(WIDE ? 64 * kWideWaves : 256) void decode_combine_kernel(AttnParams p) {
   constexpr int DPW = D / 64;  // d values per lane
   const int total = p.B * p.Hq * p.M;
   const int merge_wgs = WIDE ? total : (total + 3) / 4;
@@ -893,10 +911,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
       const int wa = (int)min((int64_t)W - 1, div_floor((US + seg_cost + 1) * W - 1, C));
       const int wb = (int)min((int64_t)W - 1, div_floor((UE + seg_cost) * W - 1, C));
       const int first = WIDE ? wa + wave : wa;
-      constexpr int STEP = WIDE ? 4 : 1;
+      constexpr int STEP = WIDE ? kWideWaves : 1;
       // Slots in batches with every load issued before the merge (8 per wave
-      // with a workgroup per row, so a wave's share of a long sequence's
-      // slots usually takes one round trip: +0.6 % on the token-major step);
+      // with a workgroup of 8 waves per row, so the 64 slots of a row of the
+      // token-major step, with its KV-head pairs, take one round trip);
       // slots of workgroups with an empty unit range were never written.
       constexpr int kBatch = WIDE ? 8 : 4;
       for (int w0 = first; w0 <= wb; w0 += kBatch * STEP) {
@@ -933,8 +951,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
       }
     }
     if constexpr (WIDE) {
-      __shared__ float s_mx[4], s_l[4];
-      __shared__ float s_acc[4][D];
+      __shared__ float s_mx[kWideWaves], s_l[kWideWaves];
+      __shared__ float s_acc[kWideWaves][D];
       if (lane == 0) {
         s_mx[wave] = mx;
         s_l[wave] = lsum;
@@ -943,13 +961,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnParams p) {
       for (int k = 0; k < DPW; ++k) s_acc[wave][lane + 64 * k] = acc[k];
       __syncthreads();
       if (wave != 0) return;
-      const float m_all = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+      float m_all = s_mx[0];
+#pragma unroll
+      for (int w = 1; w < kWideWaves; ++w) m_all = fmaxf(m_all, s_mx[w]);
       lsum = 0.f;
 #pragma unroll
       for (int k = 0; k < DPW; ++k) acc[k] = 0.f;
       if (m_all != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < kWideWaves; ++w) {
           const float sc = __builtin_amdgcn_exp2f(s_mx[w] - m_all);  // -inf slot: 0
           lsum += sc * s_l[w];
 #pragma unroll
@@ -1130,7 +1150,7 @@ void launch_combine(const AttnParams& p, int rows, hipStream_t stream) {
   }
   if (rows <= 512)
     hipLaunchKernelGGL((decode_combine_kernel<D, true>), dim3((unsigned)(rows + app_wgs)),
-                       dim3(256), 0, stream, p);
+                       dim3(64 * kWideWaves), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_combine_kernel<D, false>),
                        dim3((unsigned)((rows + 3) / 4 + app_wgs)), dim3(256), 0, stream, p);

@@ -318,8 +318,11 @@ int fa_flash_attn_paged_append_fwd(const void* q, void* k_pages, void* v_pages, 
  * accumulate in fp32; the softmax weights enter the P.V product as fp16
  * (2^-11 relative each). A head_map entry outside [0, KVH) yields NaN rows.
  * heads_per_kv: with a head_map, the most heads it sends to one KV head
- * (<= 0: H); ignored without one (the engine's map: ceil(H / KVH)). Heads
- * past the bound get NaN rows.
+ * (<= 0: H); ignored without one (the engine's map: ceil(H / KVH)). A map
+ * that sends more heads to a KV head breaks the bound: the heads past it get
+ * NaN rows, or correct ones where their segment's slot has room (with an
+ * even KVH and a bound of at most 8, a segment serves KV heads 2j and 2j + 1
+ * and holds 2 * heads_per_kv rows).
  * workspace: fa_decode_token_major_workspace_bytes(H, KVH, Dh, t_max,
  * heads_per_kv) bytes for any t <= t_max (0 when the shape is unsupported);
  * heads_per_kv = ceil(H / KVH) covers the engine's map.

@@ -179,13 +179,22 @@ def test_workspace_sizing_depends_on_sizes_only():
                               (64, 8, 0, True)):
         ws = lib.fa_paged_workspace_bytes(B, 64, M, 128, 8, 1025, 16, hpk)
         assert (ws > 0) == decode, (B, M, hpk)
-    # token-major decode: one sequence of t_max + 1 keys, rows = heads per KV head
-    t_max = 4095  # 256 groups x 8 KV heads = 2048 units -> 256 workgroups
-    slots = 8 + 256
+    # token-major decode: one sequence of t_max + 1 keys, 256 groups x 8 KV
+    # heads = 2048 units -> 256 workgroups. With an even KV-head count and at
+    # most 8 heads per KV head, each segment serves a pair of KV heads: 4
+    # segments + 256 slots of 2 x 5 rows. Without a bound (H = 40 rows per KV
+    # head, too many to pair) 8 segments + 256 slots of 40 rows.
+    t_max = 4095
     ws = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 5)
-    assert ws == align(slots * 5 * 128 * 4) + align(slots * 5 * 2 * 4) + 3 * 4
+    assert ws == align((4 + 256) * 10 * 128 * 4) + align((4 + 256) * 10 * 2 * 4) + 3 * 4
     ws0 = lib.fa_decode_token_major_workspace_bytes(40, 8, 128, t_max, 0)   # no bound: H rows
+    slots = 8 + 256
     assert ws0 == align(slots * 40 * 128 * 4) + align(slots * 40 * 2 * 4) + 3 * 4
+    # odd KV-head count (3: 768 units, 96 workgroups) or 9 heads per KV head: no pairs
+    assert lib.fa_decode_token_major_workspace_bytes(12, 3, 64, t_max, 4) == (
+        align((3 + 96) * 4 * 64 * 4) + align((3 + 96) * 4 * 2 * 4) + 3 * 4)
+    assert lib.fa_decode_token_major_workspace_bytes(72, 8, 128, t_max, 9) == (
+        align(slots * 9 * 128 * 4) + align(slots * 9 * 2 * 4) + 3 * 4)
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 128, 100, 5) < ws
     assert lib.fa_decode_token_major_workspace_bytes(40, 8, 96, t_max, 5) == 0
     # a batch beyond 2048 sequences: decode launches of at most 2048, one

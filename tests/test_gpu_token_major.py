@@ -2,7 +2,10 @@
 (attn_decode, scripts/deepseek_native_engine.sh:562-604, through the C entry
 fa_decode_token_major): fp32 q, fp16 [T, KVH, Dh] caches, head map h % KVH by
 default, against the fp64 oracle at the fp32-softmax tolerance. Rows past t
-are NaN-poisoned, so a read beyond the attended keys shows up as NaN."""
+are NaN-poisoned, so a read beyond the attended keys shows up as NaN. Shapes
+with an even KV-head count and at most 8 query heads per KV head run with
+KV-head pairs per segment (40/8, 64/8, 32/32, 14/2 and the uneven head map);
+12/3 and 72/8 run one KV head per segment."""
 import math
 
 import numpy as np
@@ -60,6 +63,30 @@ def test_token_major_decode_head_map_scale_and_workspace_reuse(gpu):
     ref = ora.decode_token_major_f64(q, k, v, 100, head_map=[h if i != 3 else 0 for i, h in enumerate(hm)])
     keep = [i for i in range(H) if i != 3]
     assert_close(out[keep], ref[keep], "head map with one bad entry")
+
+
+@pytest.mark.parametrize("t", [0, 33, 2500])
+def test_token_major_decode_kv_head_pairs_uneven_map(gpu, t):
+    """With an even KV-head count and at most 8 query heads per KV head, the
+    decode segments serve KV heads in pairs (2j, 2j + 1), alternating their
+    16-key groups. Here a head map gives KV head 0 seven query heads and its
+    partner one (bound 7: 14 rows per pair), KV heads 2 and 3 one and six,
+    and one entry is out of range (NaN row); the rest against the oracle."""
+    H, KVH, Dh = 16, 4, 128
+    hm = [0, 3, 0, 0, 1, 0, 3, 0, 3, 2, 0, 3, 9, 3, 0, 3]
+    assert max(hm.count(k) for k in range(KVH)) == 7
+    T = t + 20
+    q, k, v = _case(T, KVH, Dh, H, 500 + t, gpu)
+    kd, vd = k.clone(), v.clone()
+    kd[t + 1:] = float("nan")
+    vd[t + 1:] = float("nan")
+    hm_d = torch.tensor(hm, dtype=torch.int32, device=gpu)
+    out = decode_token_major(q.to(gpu), kd.to(gpu), vd.to(gpu), t, head_map=hm_d,
+                             heads_per_kv=7).cpu()
+    assert torch.isnan(out[12]).all()
+    ref = ora.decode_token_major_f64(q, k, v, t, head_map=[h if h < KVH else 0 for h in hm])
+    keep = [i for i in range(H) if i != 12]
+    assert_close(out[keep], ref[keep], f"uneven head map t={t}")
 
 
 def _large_logit_case(kind, T, KVH, Dh, H, seed):
