@@ -366,9 +366,11 @@ def bench_vendor_attention_reference(dev, iters=30):
     """PyTorch's own flash attention (scaled_dot_product_attention restricted
     to its flash backend, AOTriton on ROCm) on cfg2's shape as contiguous
     fp16 tensors (B=4, 40/8 heads, S=2048, D=128, causal, GQA), beside this
-    library's contiguous entry on the same tensors. Flops counted as for
-    cfg2 (4*D per visible pair). Reported only; not part of the attention
-    path. The math backend is never allowed: the call raises instead."""
+    library's contiguous entry on the same tensors; flops counted as for
+    cfg2 (4*D per visible pair). Then the same for one decode row per
+    sequence (the contiguous-decode extra's shape), in GB/s. Reported only;
+    not part of the attention path. The math backend is never allowed: the
+    call raises instead."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
     import torch.nn.functional as F
     B, Hq, Hk, S, D = 4, 40, 8, 2048, 128
@@ -381,9 +383,9 @@ def bench_vendor_attention_reference(dev, iters=30):
 
     def mean_ms(fn):
         t0 = time.perf_counter()
-        while time.perf_counter() - t0 < 0.1:
+        while time.perf_counter() - t0 < 0.1:  # 0.1 s of calls, each waited for
             fn()
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(iters):
@@ -408,6 +410,40 @@ def bench_vendor_attention_reference(dev, iters=30):
         res["speedup_over_torch_sdpa_flash"] = round(ms / ours_ms, 2)
     except RuntimeError as e:
         res["torch_sdpa_flash"] = {"unavailable": str(e)[:200]}
+    del q, k, v
+    # decode: one query row per sequence over contiguous K/V (the shape of the
+    # contiguous-decode extra: B=8, 64/8 heads, 16384 keys), two rotating
+    # caches so that every call reads HBM; GB/s of K/V plus q and o
+    B, Hq, Hk, N = 8, 64, 8, 16384
+    caches = [(torch.randn(B, Hk, N, D, generator=g, device=dev).half(),
+               torch.randn(B, Hk, N, D, generator=g, device=dev).half()) for _ in range(2)]
+    q = torch.randn(B, Hq, 1, D, generator=g, device=dev).half()
+    nbytes = B * Hk * N * D * 2 * 2 + 2 * B * Hq * D * 2
+    it = [0]
+
+    def rotating(fn):
+        def call():
+            kk, vv = caches[it[0] % 2]
+            it[0] += 1
+            return fn(kk, vv)
+        return call
+
+    ours_ms = mean_ms(rotating(lambda kk, vv: flash_attn(q, kk, vv, False)))
+    dec = {"shape": f"q [{B},{Hq},1,{D}], k/v [{B},{Hk},{N},{D}] fp16, non-causal",
+           "this_library_contiguous": {"ms": round(ours_ms, 4),
+                                       "gbs": round(nbytes / ours_ms / 1e6, 1)}}
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            fn = lambda kk, vv: F.scaled_dot_product_attention(q, kk, vv, is_causal=False,  # noqa: E731
+                                                               enable_gqa=True)
+            diff = (fn(*caches[0]).float() - flash_attn(q, *caches[0], False).float()).abs().max().item()
+            ms = mean_ms(rotating(fn))
+        dec["torch_sdpa_flash"] = {"ms": round(ms, 4), "gbs": round(nbytes / ms / 1e6, 1),
+                                   "max_abs_diff_vs_this_library": diff}
+        dec["speedup_over_torch_sdpa_flash"] = round(ms / ours_ms, 2)
+    except RuntimeError as e:
+        dec["torch_sdpa_flash"] = {"unavailable": str(e)[:200]}
+    res["decode"] = dec
     return res
 
 
