@@ -138,3 +138,37 @@ def test_token_major_decode_rejects_bad_calls(gpu):
     small = torch.empty(16, dtype=torch.uint8, device=gpu)
     with pytest.raises(RuntimeError, match="workspace of"):
         decode_token_major(qd, kd, vd, 3, workspace=small)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_token_major_decode_random_shapes_and_maps(gpu, seed):
+    """Seeded random shapes: KV-head counts 1-16 (even ones with at most 8
+    query heads per KV head run on KV-head pairs, the others one KV head per
+    segment), 1-12 query heads per KV head, D = 64 or 128, positions 0-6000,
+    and every other case a random head map (some KV heads unused) passed
+    with its exact bound; rows past t NaN-poisoned."""
+    rng = np.random.default_rng(7100 + seed)
+    KVH = int(rng.integers(1, 17))
+    per = int(rng.integers(1, 13))
+    H = KVH * per - int(rng.integers(0, per))  # not always a multiple of KVH
+    Dh = int(rng.choice([64, 128]))
+    t = int(rng.integers(0, 6001))
+    T = t + 1 + int(rng.integers(0, 40))
+    q, k, v = _case(T, KVH, Dh, H, 7200 + seed, gpu)
+    kd, vd = k.clone(), v.clone()
+    kd[t + 1:] = float("nan")
+    vd[t + 1:] = float("nan")
+    what = f"seed={seed} H={H} KVH={KVH} Dh={Dh} t={t}"
+    if seed % 2:
+        hm = [int(x) for x in rng.integers(0, KVH, size=H)]
+        bound = max(hm.count(j) for j in range(KVH))
+        hm_d = torch.tensor(hm, dtype=torch.int32, device=gpu)
+        out = decode_token_major(q.to(gpu), kd.to(gpu), vd.to(gpu), t, head_map=hm_d,
+                                 heads_per_kv=bound).cpu()
+        ref = ora.decode_token_major_f64(q, k, v, t, head_map=hm)
+        what += f" map bound={bound}"
+    else:
+        out = decode_token_major(q.to(gpu), kd.to(gpu), vd.to(gpu), t).cpu()
+        ref = ora.decode_token_major_f64(q, k, v, t)
+    assert torch.isfinite(out).all(), what
+    assert_close(out, ref, what)
