@@ -446,10 +446,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(AttnParams p) {
     // register sets: RING - 1 groups are in flight while one is processed.
     // The first pass's loads leave before the head scan and the Q loads, so
     // the segment's first K/V bytes are in flight during both.
-    // Four blocks at D = 128 compute four times as long per group, so one
-    // group in flight covers the load latency and keeps the accumulators in
-    // registers.
-    constexpr int RING = NBLK >= 4 && D == 128 ? 2 : 3;
+    // Two or four blocks at D = 128 compute two or four times as long per
+    // group, so one group in flight covers the load latency and keeps the
+    // accumulators in registers (two blocks, M = 4 over cfg4's pool: 5768
+    // against 5699 GB/s with two groups in flight).
+    constexpr int RING = NBLK >= 2 && D == 128 ? 2 : 3;
     DecodeRegs<D> ring[RING];
     // Row stride: 2D bytes in pages and contiguous K/V; the fp32-query
     // (token-major) variant reads rows Hk*D apart. A compile-time 2D keeps
